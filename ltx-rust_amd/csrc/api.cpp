@@ -1,0 +1,398 @@
+// C ABI of ltxw (include/ltxw.h): context, device memory, staged uploads and
+// the dequant / fused dequant + LoRA entry points.
+//
+// Validation mirrors the reference's error conventions (crates/ltx-weights/
+// src/error.rs:7-100): every failure is a status code plus a message, nothing
+// throws or aborts across the boundary.
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "kernels.h"
+#include "ltxw.h"
+
+struct ltxw_ctx {
+  int device = 0;
+  hipStream_t compute = nullptr;
+  hipStream_t copy = nullptr;
+  // Pinned staging ring for host -> device uploads.
+  std::vector<void*> stage;
+  std::vector<hipEvent_t> stage_done;
+  size_t stage_bytes = 0;
+  size_t next_stage = 0;
+  // Job tables of grouped launches: pinned host mirror -> device buffer.
+  void* table_host = nullptr;
+  void* table_dev = nullptr;
+  size_t table_cap = 0;
+  hipEvent_t table_done = nullptr;
+  std::string err;
+};
+
+namespace {
+
+thread_local std::string g_create_err;
+
+int fail(ltxw_ctx* ctx, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (ctx) ctx->err = buf; else g_create_err = buf;
+  return code;
+}
+
+int hip_fail(ltxw_ctx* ctx, hipError_t e, const char* what) {
+  return fail(ctx, LTXW_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(ctx, expr, what)                    \
+  do {                                              \
+    hipError_t e_ = (expr);                         \
+    if (e_ != hipSuccess) return hip_fail(ctx, e_, what); \
+  } while (0)
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// rows * cols without overflow; false when either is negative or it overflows.
+bool elem_count(int64_t rows, int64_t cols, uint64_t* n) {
+  if (rows < 0 || cols < 0) return false;
+  if (rows != 0 && (uint64_t)cols > UINT64_MAX / (uint64_t)rows) return false;
+  *n = (uint64_t)rows * (uint64_t)cols;
+  return *n <= (uint64_t)INT64_MAX / 4;
+}
+
+// Common checks of one tensor description; message names the offending field.
+int check_desc(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t* n) {
+  if (!elem_count(d.rows, d.cols, n))
+    return fail(ctx, LTXW_ERR_INVALID_ARG, "invalid shape [%lld, %lld]", (long long)d.rows, (long long)d.cols);
+  if (d.fmt != LTXW_FMT_E4M3FN && d.fmt != LTXW_FMT_E5M2)
+    return fail(ctx, LTXW_ERR_UNSUPPORTED, "unsupported FP8 format %d", d.fmt);
+  if (d.scale_mode < LTXW_SCALE_NONE || d.scale_mode > LTXW_SCALE_ROW)
+    return fail(ctx, LTXW_ERR_INVALID_ARG, "invalid scale mode %d", d.scale_mode);
+  if (d.out_dtype != LTXW_OUT_BF16 && d.out_dtype != LTXW_OUT_F32)
+    return fail(ctx, LTXW_ERR_INVALID_ARG, "invalid output dtype %d", d.out_dtype);
+  if (d.n_loras < 0 || d.n_loras > LTXW_MAX_LORAS)
+    return fail(ctx, LTXW_ERR_INVALID_ARG, "n_loras %d outside [0, %d]", d.n_loras, LTXW_MAX_LORAS);
+  if (*n == 0) return LTXW_OK;
+  if (!d.w || !d.out) return fail(ctx, LTXW_ERR_INVALID_ARG, "null weight or output pointer");
+  if (d.scale_mode != LTXW_SCALE_NONE && !d.scales)
+    return fail(ctx, LTXW_ERR_INVALID_ARG, "scale mode %d needs a scales pointer", d.scale_mode);
+  for (int l = 0; l < d.n_loras; ++l) {
+    const ltxw_lora& L = d.loras[l];
+    // store.rs:578-587: a zero rank is a rank mismatch.
+    if (L.rank <= 0)
+      return fail(ctx, LTXW_ERR_LORA_RANK, "LoRA %d has rank %d", l, L.rank);
+    if (!L.a || !L.b) return fail(ctx, LTXW_ERR_INVALID_ARG, "LoRA %d has a null factor", l);
+  }
+  return LTXW_OK;
+}
+
+ltxw::JobDev to_job(const ltxw_tensor_desc& d) {
+  ltxw::JobDev j{};
+  j.w = d.w;
+  j.out = d.out;
+  j.scales = d.scales;
+  j.rows = d.rows;
+  j.cols = d.cols;
+  j.fmt = d.fmt;
+  j.scale_mode = d.scale_mode;
+  j.n_loras = d.n_loras;
+  for (int l = 0; l < d.n_loras; ++l) j.lora[l] = {d.loras[l].b, d.loras[l].a, d.loras[l].rank, d.loras[l].coeff};
+  j.tiles_n = (int32_t)((d.cols + ltxw::kTileN - 1) / ltxw::kTileN);
+  return j;
+}
+
+// The tiled MFMA kernel's layout requirements (else: generic kernel).
+bool fused_ok(const ltxw_tensor_desc& d) {
+  if (d.cols % 8 != 0 || !aligned(d.w, 16) || !aligned(d.out, 16)) return false;
+  int64_t tiles_n = (d.cols + ltxw::kTileN - 1) / ltxw::kTileN;
+  if (tiles_n > INT32_MAX) return false;
+  for (int l = 0; l < d.n_loras; ++l)
+    if (d.loras[l].rank % 8 != 0 || !aligned(d.loras[l].a, 16) || !aligned(d.loras[l].b, 16)) return false;
+  return true;
+}
+
+int run_generic(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t begin, uint64_t count) {
+  ltxw::GenericArgs g{};
+  g.job = to_job(d);
+  g.elem_begin = begin;
+  g.elem_count = count;
+  HIP_TRY(ctx, ltxw::launch_generic(g, d.out_dtype == LTXW_OUT_F32, ctx->compute), "generic kernel launch");
+  return LTXW_OK;
+}
+
+// Dequant without LoRA: vector kernel on 16-element chunks, generic on the rest.
+int run_dequant(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t n) {
+  bool vec = aligned(d.w, 16) && aligned(d.out, 16) && (d.scale_mode != LTXW_SCALE_ROW || d.cols >= 16);
+  uint64_t chunks = vec ? n / 16 : 0;
+  if (chunks) {
+    ltxw::DequantArgs a{d.w, d.out, d.scales, n, (uint64_t)d.cols, chunks};
+    HIP_TRY(ctx, ltxw::launch_dequant(a, d.fmt, d.scale_mode, d.out_dtype == LTXW_OUT_F32, ctx->compute),
+            "dequant kernel launch");
+  }
+  if (chunks * 16 < n) return run_generic(ctx, d, chunks * 16, n - chunks * 16);
+  return LTXW_OK;
+}
+
+// Grows the grouped-launch job table (pinned host + device) to `bytes`.
+int ensure_table(ltxw_ctx* ctx, size_t bytes) {
+  if (bytes <= ctx->table_cap) {
+    HIP_TRY(ctx, hipEventSynchronize(ctx->table_done), "job table wait");
+    return LTXW_OK;
+  }
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->compute), "job table resize");
+  if (ctx->table_host) (void)hipHostFree(ctx->table_host);
+  if (ctx->table_dev) (void)hipFree(ctx->table_dev);
+  ctx->table_host = ctx->table_dev = nullptr;
+  ctx->table_cap = 0;
+  size_t cap = std::max<size_t>(bytes, 64 * 1024);
+  if (hipHostMalloc(&ctx->table_host, cap, hipHostMallocDefault) != hipSuccess)
+    return fail(ctx, LTXW_ERR_OOM, "pinned job table of %zu bytes", cap);
+  if (hipMalloc(&ctx->table_dev, cap) != hipSuccess)
+    return fail(ctx, LTXW_ERR_OOM, "device job table of %zu bytes", cap);
+  ctx->table_cap = cap;
+  return LTXW_OK;
+}
+
+// One fused launch over `jobs` (all fused_ok, same out dtype and multi flag).
+int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool multi) {
+  if (jobs.empty()) return LTXW_OK;
+  int64_t tiles = 0;
+  for (auto& j : jobs) {
+    j.tile_begin = tiles;
+    int64_t tiles_m = (j.rows + ltxw::kTileM - 1) / ltxw::kTileM;
+    tiles += tiles_m * j.tiles_n;
+  }
+  if (tiles > INT32_MAX) return fail(ctx, LTXW_ERR_INVALID_ARG, "launch of %lld tiles is too large", (long long)tiles);
+  ltxw::JobTable t{};
+  t.n_jobs = (int32_t)jobs.size();
+  t.total_tiles = tiles;
+  if (jobs.size() == 1) {
+    t.one = jobs[0];
+  } else {
+    size_t jb = jobs.size() * sizeof(ltxw::JobDev);
+    size_t bb = jobs.size() * sizeof(int64_t);
+    size_t off_b = (jb + 255) & ~size_t(255);
+    int rc = ensure_table(ctx, off_b + bb);
+    if (rc) return rc;
+    memcpy(ctx->table_host, jobs.data(), jb);
+    int64_t* begins = reinterpret_cast<int64_t*>((char*)ctx->table_host + off_b);
+    for (size_t k = 0; k < jobs.size(); ++k) begins[k] = jobs[k].tile_begin;
+    HIP_TRY(ctx, hipMemcpyAsync(ctx->table_dev, ctx->table_host, off_b + bb, hipMemcpyHostToDevice, ctx->compute),
+            "job table upload");
+    HIP_TRY(ctx, hipEventRecord(ctx->table_done, ctx->compute), "job table event");
+    t.jobs = reinterpret_cast<const ltxw::JobDev*>(ctx->table_dev);
+    t.begins = reinterpret_cast<const int64_t*>((char*)ctx->table_dev + off_b);
+  }
+  HIP_TRY(ctx, ltxw::launch_fused(t, f32out, multi, ctx->compute), "fused kernel launch");
+  return LTXW_OK;
+}
+
+int run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n) {
+  // Validate everything before queuing anything.
+  std::vector<uint64_t> counts((size_t)n);
+  for (int k = 0; k < n; ++k) {
+    int rc = check_desc(ctx, descs[k], &counts[(size_t)k]);
+    if (rc) return rc;
+  }
+  // Four fused buckets: (f32 out, multi-LoRA).
+  std::vector<ltxw::JobDev> bucket[2][2];
+  for (int k = 0; k < n; ++k) {
+    const ltxw_tensor_desc& d = descs[k];
+    uint64_t cnt = counts[(size_t)k];
+    if (cnt == 0) continue;
+    int rc = LTXW_OK;
+    if (d.n_loras == 0) {
+      rc = run_dequant(ctx, d, cnt);
+    } else if (fused_ok(d)) {
+      bucket[d.out_dtype == LTXW_OUT_F32][d.n_loras > 1].push_back(to_job(d));
+    } else {
+      rc = run_generic(ctx, d, 0, cnt);
+    }
+    if (rc) return rc;
+  }
+  for (int f = 0; f < 2; ++f)
+    for (int m = 0; m < 2; ++m) {
+      int rc = run_fused(ctx, bucket[f][m], f == 1, m == 1);
+      if (rc) return rc;
+    }
+  return LTXW_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ltxw_ctx_create(int device, size_t staging_bytes, int n_staging, ltxw_ctx** out) {
+  if (!out) return fail(nullptr, LTXW_ERR_INVALID_ARG, "null output pointer");
+  *out = nullptr;
+  int ndev = 0;
+  hipError_t e = hipGetDeviceCount(&ndev);
+  if (e != hipSuccess) return fail(nullptr, LTXW_ERR_HIP, "hipGetDeviceCount: %s", hipGetErrorString(e));
+  if (device < 0 || device >= ndev)
+    return fail(nullptr, LTXW_ERR_INVALID_ARG, "device %d not in [0, %d)", device, ndev);
+  if (staging_bytes == 0) staging_bytes = 64u << 20;
+  if (n_staging <= 0) n_staging = 4;
+  ltxw_ctx* c = new (std::nothrow) ltxw_ctx();
+  if (!c) return fail(nullptr, LTXW_ERR_OOM, "context allocation");
+  c->device = device;
+  c->stage_bytes = staging_bytes;
+  auto bail = [&](int code, const char* what, hipError_t he) {
+    g_create_err = std::string(what) + ": " + hipGetErrorString(he);
+    ltxw_ctx_destroy(c);
+    return code;
+  };
+  if ((e = hipSetDevice(device)) != hipSuccess) return bail(LTXW_ERR_HIP, "hipSetDevice", e);
+  if ((e = hipStreamCreateWithFlags(&c->compute, hipStreamNonBlocking)) != hipSuccess)
+    return bail(LTXW_ERR_HIP, "compute stream", e);
+  if ((e = hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking)) != hipSuccess)
+    return bail(LTXW_ERR_HIP, "copy stream", e);
+  if ((e = hipEventCreateWithFlags(&c->table_done, hipEventDisableTiming)) != hipSuccess)
+    return bail(LTXW_ERR_HIP, "event", e);
+  for (int k = 0; k < n_staging; ++k) {
+    void* p = nullptr;
+    hipEvent_t ev = nullptr;
+    if ((e = hipHostMalloc(&p, staging_bytes, hipHostMallocDefault)) != hipSuccess)
+      return bail(LTXW_ERR_OOM, "pinned staging buffer", e);
+    c->stage.push_back(p);
+    if ((e = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess)
+      return bail(LTXW_ERR_HIP, "event", e);
+    c->stage_done.push_back(ev);
+  }
+  *out = c;
+  return LTXW_OK;
+}
+
+void ltxw_ctx_destroy(ltxw_ctx* ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->compute) (void)hipStreamSynchronize(ctx->compute);
+  if (ctx->copy) (void)hipStreamSynchronize(ctx->copy);
+  for (void* p : ctx->stage) (void)hipHostFree(p);
+  for (hipEvent_t ev : ctx->stage_done) (void)hipEventDestroy(ev);
+  if (ctx->table_host) (void)hipHostFree(ctx->table_host);
+  if (ctx->table_dev) (void)hipFree(ctx->table_dev);
+  if (ctx->table_done) (void)hipEventDestroy(ctx->table_done);
+  if (ctx->compute) (void)hipStreamDestroy(ctx->compute);
+  if (ctx->copy) (void)hipStreamDestroy(ctx->copy);
+  delete ctx;
+}
+
+const char* ltxw_last_error(const ltxw_ctx* ctx) {
+  return ctx ? ctx->err.c_str() : g_create_err.c_str();
+}
+
+void* ltxw_ctx_stream(ltxw_ctx* ctx) { return ctx ? (void*)ctx->compute : nullptr; }
+
+int ltxw_alloc(ltxw_ctx* ctx, size_t bytes, void** dptr) {
+  if (!ctx || !dptr) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context or output pointer");
+  *dptr = nullptr;
+  if (bytes == 0) return LTXW_OK;
+  HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+  hipError_t e = hipMalloc(dptr, bytes);
+  if (e != hipSuccess) {
+    *dptr = nullptr;
+    (void)hipGetLastError();
+    return fail(ctx, LTXW_ERR_OOM, "device allocation of %zu bytes: %s", bytes, hipGetErrorString(e));
+  }
+  return LTXW_OK;
+}
+
+int ltxw_free(ltxw_ctx* ctx, void* dptr) {
+  if (!ctx) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context");
+  if (!dptr) return LTXW_OK;
+  // Work already queued may still read the buffer.
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->compute), "synchronize before free");
+  HIP_TRY(ctx, hipFree(dptr), "hipFree");
+  return LTXW_OK;
+}
+
+int ltxw_memset(ltxw_ctx* ctx, void* dptr, int value, size_t bytes) {
+  if (!ctx || (!dptr && bytes)) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context or pointer");
+  if (bytes == 0) return LTXW_OK;
+  HIP_TRY(ctx, hipMemsetAsync(dptr, value, bytes, ctx->compute), "hipMemsetAsync");
+  return LTXW_OK;
+}
+
+int ltxw_upload(ltxw_ctx* ctx, const void* host_src, size_t bytes, void* dst) {
+  if (!ctx) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context");
+  if (bytes == 0) return LTXW_OK;
+  if (!host_src || !dst) return fail(ctx, LTXW_ERR_INVALID_ARG, "null source or destination");
+  const char* src = (const char*)host_src;
+  size_t done = 0;
+  while (done < bytes) {
+    size_t k = ctx->next_stage;
+    ctx->next_stage = (k + 1) % ctx->stage.size();
+    size_t len = std::min(ctx->stage_bytes, bytes - done);
+    // The slot's previous copy must have left the buffer before it is refilled.
+    HIP_TRY(ctx, hipEventSynchronize(ctx->stage_done[k]), "staging wait");
+    memcpy(ctx->stage[k], src + done, len);
+    HIP_TRY(ctx, hipMemcpyAsync((char*)dst + done, ctx->stage[k], len, hipMemcpyHostToDevice, ctx->copy),
+            "hipMemcpyAsync H2D");
+    HIP_TRY(ctx, hipEventRecord(ctx->stage_done[k], ctx->copy), "staging event");
+    done += len;
+  }
+  // Later compute-stream work sees the data.
+  size_t last = (ctx->next_stage + ctx->stage.size() - 1) % ctx->stage.size();
+  HIP_TRY(ctx, hipStreamWaitEvent(ctx->compute, ctx->stage_done[last], 0), "compute waits for upload");
+  return LTXW_OK;
+}
+
+int ltxw_download(ltxw_ctx* ctx, const void* src, size_t bytes, void* host_dst) {
+  if (!ctx) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context");
+  if (bytes == 0) return LTXW_OK;
+  if (!src || !host_dst) return fail(ctx, LTXW_ERR_INVALID_ARG, "null source or destination");
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->compute), "synchronize before download");
+  HIP_TRY(ctx, hipMemcpy(host_dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  return LTXW_OK;
+}
+
+int ltxw_synchronize(ltxw_ctx* ctx) {
+  if (!ctx) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context");
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->copy), "copy stream synchronize");
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->compute), "compute stream synchronize");
+  return LTXW_OK;
+}
+
+int ltxw_dequant(ltxw_ctx* ctx, const uint8_t* w, int64_t rows, int64_t cols, int fmt,
+                 int scale_mode, const float* scales, void* out, int out_dtype) {
+  return ltxw_dequant_lora(ctx, w, rows, cols, fmt, scale_mode, scales, nullptr, 0, out, out_dtype);
+}
+
+int ltxw_dequant_lora(ltxw_ctx* ctx, const uint8_t* w, int64_t rows, int64_t cols, int fmt,
+                      int scale_mode, const float* scales, const ltxw_lora* loras,
+                      int n_loras, void* out, int out_dtype) {
+  if (!ctx) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context");
+  if (n_loras < 0 || n_loras > LTXW_MAX_LORAS)
+    return fail(ctx, LTXW_ERR_INVALID_ARG, "n_loras %d outside [0, %d]", n_loras, LTXW_MAX_LORAS);
+  if (n_loras > 0 && !loras) return fail(ctx, LTXW_ERR_INVALID_ARG, "null LoRA array");
+  ltxw_tensor_desc d{};
+  d.w = w;
+  d.out = out;
+  d.scales = scales;
+  d.rows = rows;
+  d.cols = cols;
+  d.fmt = fmt;
+  d.scale_mode = scale_mode;
+  d.out_dtype = out_dtype;
+  d.n_loras = n_loras;
+  for (int l = 0; l < n_loras; ++l) d.loras[l] = loras[l];
+  return run_descs(ctx, &d, 1);
+}
+
+int ltxw_dequant_lora_grouped(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n) {
+  if (!ctx) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context");
+  if (n < 0 || (n > 0 && !descs)) return fail(ctx, LTXW_ERR_INVALID_ARG, "invalid descriptor array");
+  return run_descs(ctx, descs, n);
+}
+
+}  // extern "C"

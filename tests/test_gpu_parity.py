@@ -1,0 +1,238 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle.
+
+Bars: dequantisation is bit-exact in bf16 and f32 (NaN encodings included);
+the fused LoRA merge follows the tolerance in gpu_util.compare_lora_bf16
+(1 bf16 ulp, an f32-error escape for ill-conditioned elements, Frobenius
+<= 1e-3 against the bf16-rounded f64 oracle). The generic kernel follows the
+reference's operation order and must be bit-exact.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import gpu_util as U
+import ltx_weights as lw
+from ltx_weights import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def log(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = lw.Context(0)
+    yield c
+    c.close()
+
+
+def run_case(ctx, case, out_dtype=lw.OUT_BF16, **kw):
+    d = U.Dev(ctx, case, out_dtype, **kw)
+    try:
+        d.run()
+        return d.result()
+    finally:
+        d.free()
+
+
+def all_codes_case(fmt, scale_mode, rows=64, cols=256, with_inf=True, loras=()):
+    """Every byte value in every row, rotated per row."""
+    w = np.array([np.roll(np.arange(256, dtype=np.uint8), r) for r in range(rows)])[:, :cols]
+    rng = np.random.default_rng(77)
+    return {"w": np.ascontiguousarray(w), "scales": synth.scales(rng, rows, scale_mode), "loras": list(loras),
+            "rows": rows, "cols": cols, "fmt": fmt, "scale_mode": scale_mode}
+
+
+@pytest.mark.parametrize("fmt", [lw.FMT_E4M3FN, lw.FMT_E5M2])
+@pytest.mark.parametrize("scale_mode", [lw.SCALE_NONE, lw.SCALE_TENSOR, lw.SCALE_ROW])
+@pytest.mark.parametrize("out_dtype", [lw.OUT_BF16, lw.OUT_F32])
+def test_dequant_all_codes_bit_exact(ctx, fmt, scale_mode, out_dtype):
+    log("case: all codes", fmt, scale_mode, out_dtype)
+    case = all_codes_case(fmt, scale_mode)
+    got = run_case(ctx, case, out_dtype)
+    ref = U.oracle_bf16(case) if out_dtype == lw.OUT_BF16 else U.oracle_f32(case)
+    assert np.array_equal(got.view(np.uint16 if out_dtype == lw.OUT_BF16 else np.uint32),
+                          ref.view(np.uint16 if out_dtype == lw.OUT_BF16 else np.uint32))
+
+
+def test_dequant_4096_per_tensor_scale_bit_exact(ctx):
+    """4096 x 4096 e4m3fn with one f32 scale from U[1e-3, 1e-1], bf16 out."""
+    log("case: dequant 4096x4096 tensor scale")
+    case = synth.tensor_case(1001, 4096, 4096, synth.E4M3FN, synth.SCALE_TENSOR, loras=())
+    got = run_case(ctx, case)
+    ref = U.oracle_bf16(case)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("shape", [(1, 1), (3, 17), (7, 4104), (129, 33), (2, 8), (5, 15), (1, 4097), (64, 16)])
+@pytest.mark.parametrize("scale_mode", [lw.SCALE_NONE, lw.SCALE_TENSOR, lw.SCALE_ROW])
+def test_dequant_ragged_shapes_bit_exact(ctx, shape, scale_mode):
+    log("case: ragged", shape, scale_mode)
+    case = synth.tensor_case(7, shape[0], shape[1], synth.E5M2, scale_mode, loras=())
+    got = run_case(ctx, case)
+    assert np.array_equal(got, U.oracle_bf16(case))
+
+
+@pytest.mark.parametrize("w_offset,out_offset", [(1, 0), (0, 2), (3, 6), (8, 0)])
+def test_dequant_unaligned_pointers_bit_exact(ctx, w_offset, out_offset):
+    log("case: unaligned", w_offset, out_offset)
+    case = synth.tensor_case(8, 33, 100, synth.E4M3FN, synth.SCALE_ROW, loras=())
+    got = run_case(ctx, case, w_offset=w_offset, out_offset=out_offset)
+    assert np.array_equal(got, U.oracle_bf16(case))
+
+
+def test_fused_4096_rank64_row_scale(ctx):
+    """4096 x 4096 e4m3fn, per-row scales, rank-64 bf16 LoRA, alpha = 1."""
+    log("case: fused 4096x4096 r64")
+    case = synth.tensor_case(1002, 4096, 4096, synth.E4M3FN, synth.SCALE_ROW, loras=((64, 1.0),))
+    got = run_case(ctx, case)
+    stats = U.compare_lora_bf16(case, got)
+    log("stats", stats)
+
+
+@pytest.mark.parametrize("rows,cols,ranks,fmt,scale_mode", [
+    (4104, 512, ((64, 1.0),), synth.E4M3FN, synth.SCALE_ROW),      # row tail
+    (256, 4104, ((64, 1.0),), synth.E4M3FN, synth.SCALE_TENSOR),   # column tail (4104 = 8 mod 16)
+    (130, 264, ((16, 0.5),), synth.E5M2, synth.SCALE_ROW),
+    (96, 136, ((8, 2.0),), synth.E4M3FN, synth.SCALE_NONE),
+    (200, 384, ((128, 0.5),), synth.E4M3FN, synth.SCALE_ROW),      # two K passes
+    (300, 520, ((32, 1.0), (128, 0.5)), synth.E5M2, synth.SCALE_ROW),   # stacked LoRAs
+    (128, 128, ((64, 1.0), (8, -0.25), (16, 0.75)), synth.E4M3FN, synth.SCALE_TENSOR),
+    (1, 8, ((8, 1.0),), synth.E4M3FN, synth.SCALE_ROW),
+])
+def test_fused_shapes(ctx, rows, cols, ranks, fmt, scale_mode):
+    log("case: fused", rows, cols, ranks, fmt, scale_mode)
+    case = synth.tensor_case(rows * 31 + cols, rows, cols, fmt, scale_mode, loras=ranks)
+    got = run_case(ctx, case)
+    U.compare_lora_bf16(case, got)
+
+
+def test_fused_f32_output(ctx):
+    """f32 output (the reference's own HostTensor type): within the f32
+    forward-error bound of both orders, 2*(rank+4)*2^-24*(|deq|+sum|cBA|)."""
+    log("case: fused f32 out")
+    case = synth.tensor_case(55, 512, 1024, synth.E4M3FN, synth.SCALE_ROW, loras=((64, 1.0),))
+    got = run_case(ctx, case, lw.OUT_F32).astype(np.float64)
+    ref = U.oracle_f32(case).astype(np.float64)
+    w, f, m, s, loras = U.oracle_args(case)
+    import oracle_lib as O
+    bound = O.abs_bound_rows(w, f, m, s, loras)
+    assert np.all(np.abs(got - ref) <= 2 * (64 + 4) * 2.0 ** -24 * bound)
+
+
+@pytest.mark.parametrize("rows,cols,ranks", [(9, 13, ((2, 0.75),)), (40, 100, ((3, 1.0), (5, 0.5))), (16, 24, ((4, 1.5),))])
+def test_generic_path_bit_exact(ctx, rows, cols, ranks):
+    """Ranks or widths the tiled kernel does not take run in the reference's
+    own operation order, so the result is bit-identical to the oracle."""
+    log("case: generic", rows, cols, ranks)
+    case = synth.tensor_case(rows + cols, rows, cols, synth.E4M3FN, synth.SCALE_ROW, loras=ranks)
+    for out_dtype in (lw.OUT_BF16, lw.OUT_F32):
+        got = run_case(ctx, case, out_dtype)
+        ref = U.oracle_bf16(case) if out_dtype == lw.OUT_BF16 else U.oracle_f32(case)
+        assert np.array_equal(got.view(np.uint16 if out_dtype == lw.OUT_BF16 else np.uint32),
+                              ref.view(np.uint16 if out_dtype == lw.OUT_BF16 else np.uint32))
+
+
+def test_fused_nan_inf_codes(ctx):
+    """NaN and Inf codes through the fused path: NaN stays the reference's
+    f32::NAN (bf16 0x7FC0), +-Inf plus a finite delta stays +-Inf."""
+    log("case: fused nan/inf")
+    rng = np.random.default_rng(5)
+    b, a = synth.lora_factors(rng, 64, 256, 16)
+    case = all_codes_case(lw.FMT_E5M2, lw.SCALE_ROW, loras=[(b, a, 16, 1.0)])
+    got = run_case(ctx, case)
+    U.compare_lora_bf16(case, got)
+
+
+def test_grouped_block_matches_single_calls(ctx):
+    """A grouped launch over mixed tensors equals per-tensor calls bit for bit."""
+    log("case: grouped vs single")
+    cases = [
+        synth.tensor_case(11, 256, 512, synth.E4M3FN, synth.SCALE_ROW, loras=((64, 1.0),)),
+        synth.tensor_case(12, 384, 256, synth.E5M2, synth.SCALE_TENSOR, loras=((32, 1.0), (16, 0.5))),
+        synth.tensor_case(13, 100, 72, synth.E4M3FN, synth.SCALE_ROW, loras=((8, 1.0),)),
+        synth.tensor_case(14, 64, 64, synth.E4M3FN, synth.SCALE_NONE, loras=()),
+        synth.tensor_case(15, 33, 21, synth.E4M3FN, synth.SCALE_ROW, loras=((2, 0.5),)),
+    ]
+    devs = [U.Dev(ctx, c) for c in cases]
+    try:
+        singles = []
+        for d in devs:
+            d.run()
+            singles.append(d.result())
+        for d in devs:
+            ctx.memset(d.out, 0xFF, d.n * d.ob)
+        ctx.grouped([{"w": d.w, "out": d.out, "scales": d.s, "rows": d.case["rows"], "cols": d.case["cols"],
+                      "fmt": d.case["fmt"], "scale_mode": d.case["scale_mode"], "loras": d.loras} for d in devs])
+        for d, s in zip(devs, singles):
+            assert np.array_equal(d.result(), s)
+    finally:
+        for d in devs:
+            d.free()
+
+
+def test_dit_block_sampled_rows(ctx):
+    """One DiT block (8 x 4096^2, 16384 x 4096, 4096 x 16384), per-row scales,
+    rank-64 LoRA on every tensor, materialised in one grouped call; each tensor
+    checked against the oracle on 96 sampled rows plus the first and last."""
+    log("case: DiT block")
+    rng = np.random.default_rng(0)
+    cases, devs = [], []
+    try:
+        for k, (name, rows, cols) in enumerate(synth.BLOCK_LINEARS):
+            c = synth.tensor_case(3000 + k, rows, cols, synth.E4M3FN, synth.SCALE_ROW, loras=((64, 1.0),))
+            cases.append(c)
+            devs.append(U.Dev(ctx, c))
+        ctx.grouped([{"w": d.w, "out": d.out, "scales": d.s, "rows": d.case["rows"], "cols": d.case["cols"],
+                      "fmt": d.case["fmt"], "scale_mode": d.case["scale_mode"], "loras": d.loras} for d in devs])
+        for d, c in zip(devs, cases):
+            got = d.result()
+            sel = np.unique(np.concatenate([[0, c["rows"] - 1], rng.choice(c["rows"], 96, replace=False)]))
+            U.compare_lora_bf16(c, got[sel], row_sel=sel)
+    finally:
+        for d in devs:
+            d.free()
+
+
+def test_invalid_arguments_report_status(ctx):
+    log("case: errors")
+    p = ctx.alloc(1024)
+    try:
+        with pytest.raises(lw.InvalidArgument):
+            ctx.dequant(p, -1, 4, lw.FMT_E4M3FN, lw.SCALE_NONE, None, p)
+        with pytest.raises(lw.UnsupportedDtype):
+            ctx.dequant(p, 4, 4, 7, lw.SCALE_NONE, None, p)
+        with pytest.raises(lw.InvalidArgument):
+            ctx.dequant(p, 4, 4, lw.FMT_E4M3FN, lw.SCALE_ROW, None, p)
+        with pytest.raises(lw.InvalidArgument):
+            ctx.dequant(None, 4, 4, lw.FMT_E4M3FN, lw.SCALE_NONE, None, p)
+        with pytest.raises(lw.LoraRankMismatch):
+            ctx.dequant_lora(p, 4, 4, lw.FMT_E4M3FN, lw.SCALE_NONE, None, [(p, p, 0, 1.0)], p)
+        with pytest.raises(lw.InvalidArgument):
+            ctx.dequant_lora(p, 4, 4, lw.FMT_E4M3FN, lw.SCALE_NONE, None, [(p, p, 1, 1.0)] * 5, p)
+        with pytest.raises(lw.InvalidArgument):
+            ctx.dequant(p, 1 << 40, 1 << 40, lw.FMT_E4M3FN, lw.SCALE_NONE, None, p)
+        with pytest.raises(lw.OutOfMemory):
+            ctx.alloc(1 << 50)
+        ctx.dequant(p, 0, 4, lw.FMT_E4M3FN, lw.SCALE_NONE, None, p)  # empty: no-op
+        ctx.synchronize()
+    finally:
+        ctx.free(p)
+
+
+def test_upload_download_round_trip(ctx):
+    log("case: round trip")
+    rng = np.random.default_rng(1)
+    x = rng.integers(0, 256, size=(3 << 20) + 7, dtype=np.uint8)
+    p = ctx.alloc(x.nbytes)
+    try:
+        ctx.upload(x, p)
+        y = np.empty_like(x)
+        ctx.download(p, y)
+        assert np.array_equal(x, y)
+    finally:
+        ctx.free(p)
