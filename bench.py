@@ -1,0 +1,308 @@
+"""Benchmark: fused FP8 dequant + LoRA merge on one MI355X.
+
+Workload (one step = one fused dequant + merge of one DiT linear layer):
+  W 4096 (out) x 4096 (in) e4m3fn, per-output-row f32 scales U[1e-3, 1e-1],
+  LoRA B 4096 x 64 and A 64 x 4096 bf16 ~ N(0, 0.02^2), alpha = 1, bf16 out.
+Inputs are resident in HBM before timing; consecutive steps rotate over
+>= 1 GiB of distinct buffers so the 256 MB MALL cannot serve repeats.
+
+value     = algorithmic bytes per step * steps / timed seconds (GB/s), with
+            algorithmic bytes = out*in (FP8) + 2*out*in (bf16 out) + 4*out
+            (scales) + 2*r*(out+in) (bf16 factors).
+roofline  = that figure against MI355X's 8 TB/s HBM peak; `traffic` is the
+            rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch (scaled by the
+            same counters on a plain device copy) from profiles/, when present.
+cpu_baseline = the CPU oracle (a C restatement of the reference's read path,
+            same operation order) on the same layer, on this host's cores.
+
+Prints exactly one JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "ltx-rust_amd"))
+
+import numpy as np  # noqa: E402
+
+METRIC = "dequant+LoRA-merge GB/s & % HBM roofline; s to materialise 22B weights"
+HBM_PEAK_GBPS = 8000.0
+ROWS, COLS, RANK = 4096, 4096, 64
+ROTATE_BYTES = 1 << 30
+PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "fused_dequant_lora_4096x4096_r64.pmc.txt")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Hip:
+    """The few HIP runtime calls the bench needs (events, device copies)."""
+
+    def __init__(self):
+        self.L = ctypes.CDLL("libamdhip64.so")
+        self.L.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.L.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.L.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.L.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.L.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.L.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+
+    def _ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed with HIP error {rc}")
+
+    def event(self):
+        e = ctypes.c_void_p()
+        self._ok(self.L.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
+        return e
+
+    def record(self, e, stream):
+        self._ok(self.L.hipEventRecord(e, stream), "hipEventRecord")
+
+    def elapsed_ms(self, a, b):
+        self._ok(self.L.hipEventSynchronize(b), "hipEventSynchronize")
+        ms = ctypes.c_float()
+        self._ok(self.L.hipEventElapsedTime(ctypes.byref(ms), a, b), "hipEventElapsedTime")
+        return ms.value
+
+    def copy_d2d(self, dst, src, n, stream):
+        self._ok(self.L.hipMemcpyAsync(dst, src, n, 3, stream), "hipMemcpyAsync D2D")
+
+
+def read_traffic():
+    """Per-dispatch HBM bytes from the committed rocprofv3 PMC summary."""
+    if not os.path.exists(PROFILE_SUMMARY):
+        return None
+    vals = {}
+    with open(PROFILE_SUMMARY) as f:
+        for line in f:
+            if ":" in line and line.strip().startswith("traffic_bytes_per_dispatch"):
+                try:
+                    vals["traffic"] = float(line.split(":", 1)[1].split()[0])
+                except ValueError:
+                    pass
+    return vals.get("traffic")
+
+
+def cpu_baseline(case, budget_s):
+    """The oracle on the same tensor, all host threads, repeated to ~budget_s."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+
+    threads = min(16, os.cpu_count() or 1)
+    loras = [(b, a, O.BF16, c) for (b, a, r, c) in case["loras"]]
+    fmt = O.E4M3FN if case["fmt"] == 0 else O.E5M2
+    args = (case["w"], fmt, case["scale_mode"], case["scales"], loras)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        O.read_bf16(*args, threads=threads)
+        reps += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return threads, reps, dt
+
+
+def workload_cases(name, synth):
+    """The tensors one step materialises, as synth.tensor_case dicts."""
+    if name == "layer":
+        return [synth.tensor_case(1002, ROWS, COLS, synth.E4M3FN, synth.SCALE_ROW, loras=((RANK, 1.0),))]
+    if name == "dequant":
+        return [synth.tensor_case(1001, ROWS, COLS, synth.E4M3FN, synth.SCALE_TENSOR, loras=())]
+    if name == "block":
+        return [synth.tensor_case(1003 * 100 + k, r, c, synth.E4M3FN, synth.SCALE_ROW, loras=((RANK, 1.0),))
+                for k, (_, r, c) in enumerate(synth.BLOCK_LINEARS)]
+    if name == "mixed":
+        out = []
+        for k, (nm, r, c) in enumerate(synth.BLOCK_LINEARS):
+            ffn = nm.startswith("ff.")
+            out.append(synth.tensor_case(1005 * 100 + k, r, c, synth.E5M2 if ffn else synth.E4M3FN,
+                                         synth.SCALE_ROW if ffn else synth.SCALE_TENSOR,
+                                         loras=((32, 1.0), (128, 0.5))))
+        out.append(synth.tensor_case(1005 * 100 + 20, 4096, 4104, synth.E4M3FN, synth.SCALE_TENSOR,
+                                     loras=((32, 1.0), (128, 0.5))))
+        out.append(synth.tensor_case(1005 * 100 + 21, 4104, 16384, synth.E5M2, synth.SCALE_ROW,
+                                     loras=((32, 1.0), (128, 0.5))))
+        return out
+    raise SystemExit(f"unknown workload {name}")
+
+
+WORKLOAD_TEXT = {
+    "layer": "fused FP8 dequant + rank-64 LoRA merge, one 4096x4096 DiT linear, e4m3fn, per-row scales, bf16 out",
+    "dequant": "FP8 e4m3fn -> bf16 dequant, one 4096x4096 tensor, per-tensor scale",
+    "block": "fused dequant + rank-64 LoRA, one DiT block (8 x 4096^2, 16384x4096, 4096x16384), per-row scales, one grouped call",
+    "mixed": "DiT block with e5m2 FFN (row scales) / e4m3fn attention (tensor scale), LoRAs r32 a=1 + r128 a=0.5, plus 4096x4104 and 4104x16384",
+}
+
+
+def tensor_arrays(c):
+    """Host arrays of one case in upload order: weight, [scales], (B, A) per LoRA."""
+    arrs = [c["w"]] + ([c["scales"]] if c["scales"] is not None else [])
+    for b, a, _, _ in c["loras"]:
+        arrs += [b, a]
+    return arrs
+
+
+def build_instances(ctx, cases, hip, stream, rotate_bytes=ROTATE_BYTES):
+    """Device copies of the workload, repeated until they span rotate_bytes.
+    Returns (instances, allocations, count); an instance is the list of
+    grouped-call descriptors of one copy."""
+    inst_bytes = sum(sum(x.nbytes for x in tensor_arrays(c)) + c["rows"] * c["cols"] * 2 for c in cases)
+    n_inst = max(2, -(-rotate_bytes // inst_bytes))
+    insts, allocs, nbytes_of = [], [], {}
+    for k in range(n_inst):
+        descs = []
+        for ci, c in enumerate(cases):
+            ptrs = []
+            for x in tensor_arrays(c):
+                p = ctx.alloc(x.nbytes)
+                allocs.append(p)
+                nbytes_of[p] = x.nbytes
+                if k == 0:
+                    ctx.upload(x, p)
+                ptrs.append(p)
+            if k > 0:
+                for dst, sp, x in zip(ptrs, insts[0][ci]["_ptrs"], tensor_arrays(c)):
+                    hip.copy_d2d(dst, sp, x.nbytes, stream)
+            out = ctx.alloc(c["rows"] * c["cols"] * 2)
+            allocs.append(out)
+            nbytes_of[out] = c["rows"] * c["cols"] * 2
+            q = 1 if c["scales"] is not None else 0
+            loras = [(ptrs[1 + q + 2 * l], ptrs[2 + q + 2 * l], r, co) for l, (_, _, r, co) in enumerate(c["loras"])]
+            for b_p, a_p, r, _ in loras:
+                assert nbytes_of[b_p] == c["rows"] * r * 2 and nbytes_of[a_p] == r * c["cols"] * 2
+            descs.append({"w": ptrs[0], "scales": ptrs[1] if q else None, "out": out, "rows": c["rows"],
+                          "cols": c["cols"], "fmt": c["fmt"], "scale_mode": c["scale_mode"], "loras": loras,
+                          "_ptrs": ptrs})
+        insts.append(descs)
+    return insts, allocs, n_inst
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="layer", choices=sorted(WORKLOAD_TEXT))
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget (0 skips it)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the weight set shards by tensor with no exchange; see the design notes).", file=sys.stderr)
+        sys.exit(2)
+
+    import ltx_weights as lw
+    from ltx_weights import synth
+
+    hip = Hip()
+    log(f"generating inputs ({args.workload})")
+    cases = workload_cases(args.workload, synth)
+    step_bytes = sum(synth.algorithmic_bytes(c["rows"], c["cols"], c["scale_mode"], [l[2] for l in c["loras"]])
+                     for c in cases)
+    flops = sum(synth.lora_flops(c["rows"], c["cols"], [l[2] for l in c["loras"]]) for c in cases)
+
+    ctx = lw.Context(0)
+    stream = ctx.stream()
+    insts, allocs, n_inst = build_instances(ctx, cases, hip, stream)
+    log(f"{n_inst} rotating instances")
+    ctx.synchronize()
+
+    def step(k):
+        ctx.grouped(insts[k % n_inst])
+
+    # Plain device copy ceiling on the same stream (read + write bytes / time).
+    cp_n = 512 << 20
+    src_p, dst_p = ctx.alloc(cp_n), ctx.alloc(cp_n)
+    e0, e1 = hip.event(), hip.event()
+    for _ in range(3):
+        hip.copy_d2d(dst_p, src_p, cp_n, stream)
+    hip.record(e0, stream)
+    for _ in range(10):
+        hip.copy_d2d(dst_p, src_p, cp_n, stream)
+    hip.record(e1, stream)
+    copy_gbps = 2 * cp_n * 10 / (hip.elapsed_ms(e0, e1) * 1e-3) / 1e9
+    ctx.free(src_p)
+    ctx.free(dst_p)
+    log(f"device copy ceiling {copy_gbps:.0f} GB/s")
+
+    log(f"warmup {args.warmup}")
+    for k in range(args.warmup):
+        step(k)
+    ctx.synchronize()
+    log(f"timing {args.steps} steps")
+    t_start, t_end = hip.event(), hip.event()
+    hip.record(t_start, stream)
+    for k in range(args.steps):
+        step(args.warmup + k)
+    hip.record(t_end, stream)
+    ms = hip.elapsed_ms(t_start, t_end)
+    ctx.synchronize()
+    per_step_s = ms * 1e-3 / args.steps
+    value = step_bytes / per_step_s / 1e9
+    log(f"{ms / args.steps * 1e3:.2f} us/step, {value:.0f} GB/s")
+
+    # Correctness spot check of the last instance written against the oracle.
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import gpu_util as U
+    last = insts[(args.warmup + args.steps - 1) % n_inst]
+    for c, d in zip(cases, last):
+        out = np.empty((c["rows"], c["cols"]), dtype=np.uint16)
+        ctx.download(d["out"], out)
+        sel = np.unique(np.linspace(0, c["rows"] - 1, 64).astype(np.int64))
+        if c["loras"]:
+            stats = U.compare_lora_bf16(c, out[sel], row_sel=sel)
+        else:
+            ref = U.oracle_bf16(c, row_sel=sel)
+            stats = {"bit_exact": bool(np.array_equal(ref, out[sel]))}
+            if not stats["bit_exact"]:
+                raise AssertionError("dequant output differs from the oracle")
+    log("parity on sampled rows (last tensor):", stats)
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        log("cpu baseline")
+        threads, reps, dt = cpu_baseline(cases[0], args.cpu_seconds)
+        c0 = cases[0]
+        b0 = synth.algorithmic_bytes(c0["rows"], c0["cols"], c0["scale_mode"], [l[2] for l in c0["loras"]])
+        cpu = {"value": round(b0 * reps / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"{reps} x the {c0['rows']}x{c0['cols']} tensor through the C oracle "
+                         f"(reference operation order), {threads} threads, {dt:.1f} s",
+               "s_per_tensor": round(dt / reps, 4)}
+
+    for p in allocs:
+        ctx.free(p)
+    ctx.close()
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded: uniform non-NaN FP8 codes, U[1e-3,1e-1] scales, N(0,0.02^2) bf16 factors)",
+        "config": {"workload": WORKLOAD_TEXT[args.workload], "name": args.workload, "tensors": len(cases),
+                   "params": int(sum(c["rows"] * c["cols"] for c in cases)), "rotating_instances": n_inst},
+        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBPS, 4),
+                     "traffic": read_traffic() if args.workload == "layer" else None,
+                     "algorithmic_bytes": step_bytes, "lora_flops": flops,
+                     "copy_ceiling_GBps": round(copy_gbps, 1), "frac_of_copy": round(value / copy_gbps, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -21,6 +21,7 @@
 
 struct ltxw_ctx {
   int device = 0;
+  int cu_count = 256;
   hipStream_t compute = nullptr;
   hipStream_t copy = nullptr;
   // Pinned staging ring for host -> device uploads.
@@ -70,6 +71,26 @@ bool elem_count(int64_t rows, int64_t cols, uint64_t* n) {
   return *n <= (uint64_t)INT64_MAX / 4;
 }
 
+// When the runtime knows the device allocation containing `p`, the launch's
+// byte extent [p, p + bytes) must lie inside it: a wrong or undersized
+// buffer is then an INVALID_ARG instead of a GPU memory fault. Pointers the
+// runtime does not track (other allocators) cannot be checked and pass.
+// Mirrors the byte-range check of `Entry::read_raw` (src/store.rs:52-73).
+int check_extent(ltxw_ctx* ctx, const void* p, uint64_t bytes, const char* what) {
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, const_cast<void*>(p)) != hipSuccess) {
+    (void)hipGetLastError();
+    return LTXW_OK;
+  }
+  uintptr_t b = (uintptr_t)base, q = (uintptr_t)p;
+  uint64_t have = (q >= b && q - b <= size) ? size - (q - b) : 0;
+  if (bytes > have)
+    return fail(ctx, LTXW_ERR_INVALID_ARG, "%s buffer holds %llu bytes from the pointer, the tensor needs %llu",
+                what, (unsigned long long)have, (unsigned long long)bytes);
+  return LTXW_OK;
+}
+
 // Common checks of one tensor description; message names the offending field.
 int check_desc(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t* n) {
   if (!elem_count(d.rows, d.cols, n))
@@ -91,7 +112,19 @@ int check_desc(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t* n) {
     // store.rs:578-587: a zero rank is a rank mismatch.
     if (L.rank <= 0)
       return fail(ctx, LTXW_ERR_LORA_RANK, "LoRA %d has rank %d", l, L.rank);
+    if (L.rank > (1 << 20)) return fail(ctx, LTXW_ERR_INVALID_ARG, "LoRA %d rank %d is too large", l, L.rank);
     if (!L.a || !L.b) return fail(ctx, LTXW_ERR_INVALID_ARG, "LoRA %d has a null factor", l);
+  }
+  int rc;
+  if ((rc = check_extent(ctx, d.w, *n, "weight"))) return rc;
+  if ((rc = check_extent(ctx, d.out, *n * (d.out_dtype == LTXW_OUT_F32 ? 4 : 2), "output"))) return rc;
+  if (d.scale_mode != LTXW_SCALE_NONE &&
+      (rc = check_extent(ctx, d.scales, 4 * (d.scale_mode == LTXW_SCALE_ROW ? (uint64_t)d.rows : 1), "scales")))
+    return rc;
+  for (int l = 0; l < d.n_loras; ++l) {
+    const ltxw_lora& L = d.loras[l];
+    if ((rc = check_extent(ctx, L.b, 2 * (uint64_t)d.rows * (uint64_t)L.rank, "LoRA B"))) return rc;
+    if ((rc = check_extent(ctx, L.a, 2 * (uint64_t)L.rank * (uint64_t)d.cols, "LoRA A"))) return rc;
   }
   return LTXW_OK;
 }
@@ -107,18 +140,20 @@ ltxw::JobDev to_job(const ltxw_tensor_desc& d) {
   j.scale_mode = d.scale_mode;
   j.n_loras = d.n_loras;
   for (int l = 0; l < d.n_loras; ++l) j.lora[l] = {d.loras[l].b, d.loras[l].a, d.loras[l].rank, d.loras[l].coeff};
-  j.tiles_n = (int32_t)((d.cols + ltxw::kTileN - 1) / ltxw::kTileN);
+  j.bands_n = (int32_t)((d.cols + ltxw::kBandCols - 1) / ltxw::kBandCols);
   return j;
 }
 
 // The tiled MFMA kernel's layout requirements (else: generic kernel).
 bool fused_ok(const ltxw_tensor_desc& d) {
   if (d.cols % 8 != 0 || !aligned(d.w, 16) || !aligned(d.out, 16)) return false;
-  int64_t tiles_n = (d.cols + ltxw::kTileN - 1) / ltxw::kTileN;
-  if (tiles_n > INT32_MAX) return false;
-  for (int l = 0; l < d.n_loras; ++l)
+  if ((d.cols + ltxw::kBandCols - 1) / ltxw::kBandCols > INT32_MAX) return false;
+  int k = 0;
+  for (int l = 0; l < d.n_loras; ++l) {
     if (d.loras[l].rank % 8 != 0 || !aligned(d.loras[l].a, 16) || !aligned(d.loras[l].b, 16)) return false;
-  return true;
+    k += ltxw::pad_rank(d.loras[l].rank);
+  }
+  return k <= ltxw::kRankMax;
 }
 
 int run_generic(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t begin, uint64_t count) {
@@ -163,19 +198,39 @@ int ensure_table(ltxw_ctx* ctx, size_t bytes) {
   return LTXW_OK;
 }
 
+// Total padded LoRA rank of a job (its K extent in the LDS stage).
+int job_k(const ltxw::JobDev& j) {
+  int k = 0;
+  for (int l = 0; l < j.n_loras; ++l) k += ltxw::pad_rank(j.lora[l].rank);
+  return k;
+}
+
 // One fused launch over `jobs` (all fused_ok, same out dtype and multi flag).
+// Strips per wave S: enough that every CU keeps about two workgroups busy
+// for the whole launch (fewer, longer-lived waves that prefetch ahead).
 int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool multi) {
   if (jobs.empty()) return LTXW_OK;
-  int64_t tiles = 0;
+  int64_t strips = 0;
+  int kmax = 0;
   for (auto& j : jobs) {
-    j.tile_begin = tiles;
-    int64_t tiles_m = (j.rows + ltxw::kTileM - 1) / ltxw::kTileM;
-    tiles += tiles_m * j.tiles_n;
+    strips += (int64_t)j.bands_n * ((j.rows + ltxw::kStripRows - 1) / ltxw::kStripRows);
+    kmax = std::max(kmax, job_k(j));
   }
-  if (tiles > INT32_MAX) return fail(ctx, LTXW_ERR_INVALID_ARG, "launch of %lld tiles is too large", (long long)tiles);
+  const int64_t target_waves = (int64_t)ctx->cu_count * 2 * ltxw::kWavesPerGroup;
+  int64_t S = std::max<int64_t>(1, (strips + target_waves - 1) / target_waves);
+  S = std::min<int64_t>(S, 1 << 20);
+  const int64_t group_rows = (int64_t)ltxw::kWavesPerGroup * S * ltxw::kStripRows;
+  int64_t units = 0;
+  for (auto& j : jobs) {
+    j.unit_begin = units;
+    units += (int64_t)j.bands_n * ((j.rows + group_rows - 1) / group_rows);
+  }
+  if (units > INT32_MAX) return fail(ctx, LTXW_ERR_INVALID_ARG, "launch of %lld work units is too large", (long long)units);
   ltxw::JobTable t{};
   t.n_jobs = (int32_t)jobs.size();
-  t.total_tiles = tiles;
+  t.strips = (int32_t)S;
+  t.total_units = units;
+  t.lds_ld = kmax + 8;
   if (jobs.size() == 1) {
     t.one = jobs[0];
   } else {
@@ -186,7 +241,7 @@ int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool 
     if (rc) return rc;
     memcpy(ctx->table_host, jobs.data(), jb);
     int64_t* begins = reinterpret_cast<int64_t*>((char*)ctx->table_host + off_b);
-    for (size_t k = 0; k < jobs.size(); ++k) begins[k] = jobs[k].tile_begin;
+    for (size_t k = 0; k < jobs.size(); ++k) begins[k] = jobs[k].unit_begin;
     HIP_TRY(ctx, hipMemcpyAsync(ctx->table_dev, ctx->table_host, off_b + bb, hipMemcpyHostToDevice, ctx->compute),
             "job table upload");
     HIP_TRY(ctx, hipEventRecord(ctx->table_done, ctx->compute), "job table event");
@@ -252,6 +307,8 @@ int ltxw_ctx_create(int device, size_t staging_bytes, int n_staging, ltxw_ctx** 
     return code;
   };
   if ((e = hipSetDevice(device)) != hipSuccess) return bail(LTXW_ERR_HIP, "hipSetDevice", e);
+  if ((e = hipDeviceGetAttribute(&c->cu_count, hipDeviceAttributeMultiprocessorCount, device)) != hipSuccess)
+    return bail(LTXW_ERR_HIP, "device attribute", e);
   if ((e = hipStreamCreateWithFlags(&c->compute, hipStreamNonBlocking)) != hipSuccess)
     return bail(LTXW_ERR_HIP, "compute stream", e);
   if ((e = hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking)) != hipSuccess)

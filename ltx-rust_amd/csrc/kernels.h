@@ -8,9 +8,16 @@ namespace ltxw {
 
 constexpr int kMaxLoras = 4;
 
-// Tile of the fused kernel: TM output rows x TN output columns per workgroup.
-constexpr int kTileM = 128;
-constexpr int kTileN = 128;
+// Work decomposition of the fused kernel. A workgroup (4 waves) owns one
+// band of kBandCols output columns and a group of 4 * S strips of kStripRows
+// rows each (S = strips per wave, chosen per launch); wave w takes strips
+// w, w + 4, w + 8, ...
+constexpr int kBandCols = 128;
+constexpr int kStripRows = 32;
+constexpr int kWavesPerGroup = 4;
+// Largest total LoRA rank (sum over a tensor's LoRAs, each padded to a
+// multiple of 32) the fused kernel stages in LDS.
+constexpr int kRankMax = 224;  // 128 slots x (224 + 8) bf16 = 59 KB of LDS
 
 struct LoraDev {
   const uint16_t* b;  // bf16 [rows x rank]
@@ -29,17 +36,19 @@ struct JobDev {
   int32_t fmt;
   int32_t scale_mode;
   int32_t n_loras;
-  int32_t tiles_n;     // tiles along cols
-  int64_t tile_begin;  // first flat tile index of this job in the launch
+  int32_t bands_n;     // column bands (ceil(cols / kBandCols))
+  int64_t unit_begin;  // first flat work unit of this job in the launch
   LoraDev lora[kMaxLoras];
 };
 
 struct JobTable {
   JobDev one;            // used when n_jobs == 1 (no device table needed)
   const JobDev* jobs;    // device array when n_jobs > 1
-  const int64_t* begins; // device array of tile_begin, ascending
+  const int64_t* begins; // device array of unit_begin, ascending
   int32_t n_jobs;
-  int64_t total_tiles;
+  int32_t strips;        // S: strips per wave
+  int64_t total_units;   // workgroups in the launch
+  int32_t lds_ld;        // AT row stride (bf16) sized for the launch's largest rank
 };
 
 struct DequantArgs {
@@ -62,9 +71,13 @@ struct GenericArgs {
 hipError_t launch_dequant(const DequantArgs& a, int fmt, int scale_mode, bool f32out,
                           hipStream_t stream);
 
-// Fused dequant + LoRA over every tile of every job. Requirements checked by
-// the caller: cols % 8 == 0, ranks % 8 == 0, all pointers 16-byte aligned.
+// Fused dequant + LoRA over every work unit of every job. Requirements checked
+// by the caller: cols % 8 == 0, ranks % 8 == 0, all pointers 16-byte aligned,
+// total padded rank <= kRankMax.
 hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, hipStream_t stream);
+
+// Padded K extent of one LoRA in the fused kernel's LDS stage.
+__host__ __device__ inline int pad_rank(int rank) { return (rank + 31) / 32 * 32; }
 
 // One thread per element, reference operation order. Any shape, alignment.
 hipError_t launch_generic(const GenericArgs& a, bool f32out, hipStream_t stream);

@@ -58,6 +58,14 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __builtin_bit_cast(float, (uint32_t)h << 16);
 }
 
+// Pointers read out of job descriptors are generic; marking them global makes
+// the compiler emit global_load/global_store (not flat_*, which also count
+// against the LDS counter and skip the global addressing modes).
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* G(T* p) {
+  return (__attribute__((address_space(1))) T*)(p);
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs; map them so that each
 // XCD takes a contiguous range of logical tiles (tiles of one row band share
 // their LoRA B rows in that XCD's L2). A bijection on [0, n).
@@ -161,193 +169,221 @@ __global__ __launch_bounds__(256) void k_generic(GenericArgs g) {
 // ---------------------------------------------------------------------------
 // (b) Fused dequant + LoRA merge.
 //
-// Workgroup: 256 threads (4 waves), output tile kTileM x kTileN = 128 x 128.
-// Wave w owns rows [32w, 32w+32) of the tile.
+// Workgroup: 4 waves. Work unit: one band of 128 output columns [i0, i0+128)
+// and 4*S strips of 32 rows; wave w walks strips w, w+4, ... of the unit.
 //
-// LoRA product on MFMA v_mfma_f32_32x32x16_bf16 with M = output column i,
-// N = output row o, K = rank r:
-//   A operand (i x r) = A_lora^T, staged transposed in LDS (AT[i][r]) from
-//                       coalesced row loads of A_lora, 64 ranks at a time;
-//   B operand (r x o) = B_lora rows, 16-byte global loads (r is contiguous);
-//   C (i x o) lane layout: lane l holds o = l%32 and, for accumulator v,
-//                       i = 8*(v/4) + 4*(l/32) + v%4 within the 32-block.
-// The f32 result is relaid through LDS (per wave, 16 rows at a time) into row
-// order so that the FP8 input (read once, 8 bytes per lane, prefetched before
-// the MFMA phase) and the bf16 output (16 bytes per lane) are coalesced:
-// 16 lanes cover 128 contiguous columns of one row.
+// LoRA product on v_mfma_f32_16x16x32_bf16 with M = output row o, N = output
+// column i, K = rank r, and the N index permuted as i = i0 + 8*n + nb for
+// N-block nb (0..7) and MFMA column n (0..15). With the C layout (lane l holds
+// column n = l%16 and rows m = 4*(l/16) + v), lane l then owns, for each of
+// its 8 rows, the 8 contiguous columns i0 + 8*(l%16) .. +7 across the 8
+// N-blocks: the FP8 input (8 bytes per lane) and the bf16 output (16 bytes per
+// lane) are read and written straight from registers, 16 lanes covering 128
+// contiguous columns of a row, with no LDS relayout.
+//   A operand (o x r): LoRA B rows, 16-byte loads (r contiguous), from L2.
+//   B operand (r x i): LoRA A transposed, staged once per work unit in LDS as
+//                      AT[slot][k] with slot = nb*16 + n (consecutive lanes
+//                      read consecutive slots: conflict-free 128-bit reads).
+// Several LoRAs are staged side by side along k (each padded to 32).
+// The FP8 bytes of the next strip are loaded while the current one computes.
 // ---------------------------------------------------------------------------
-constexpr int kKC = 64;             // ranks staged per LDS pass
-constexpr int kATLd = kKC + 8;      // AT row stride in bf16 (144 B: conflict-free b128 reads)
-constexpr int kAccLd = kTileN + 4;  // relayout row stride in f32
-
-__device__ __forceinline__ void load_job(const JobTable& t, uint64_t tile, JobDev& J) {
+__device__ __forceinline__ void load_job(const JobTable& t, uint64_t unit, JobDev& J) {
   if (t.n_jobs == 1) {
     J = t.one;
     return;
   }
-  int lo = 0, hi = t.n_jobs - 1;  // last job with begins[j] <= tile
+  int lo = 0, hi = t.n_jobs - 1;  // last job with begins[j] <= unit
   while (lo < hi) {
     int mid = (lo + hi + 1) >> 1;
-    if ((uint64_t)t.begins[mid] <= tile) lo = mid; else hi = mid - 1;
+    if ((uint64_t)G(t.begins)[mid] <= unit) lo = mid; else hi = mid - 1;
   }
-  J = t.jobs[lo];
+  // Copy the descriptor as 16-byte global loads (the table is 256-byte aligned).
+  static_assert(sizeof(JobDev) % 16 == 0, "JobDev is copied in 16-byte pieces");
+  u32x4 raw[sizeof(JobDev) / 16];
+  const auto src = G(reinterpret_cast<const u32x4*>(t.jobs + lo));
+#pragma unroll
+  for (int k = 0; k < (int)(sizeof(JobDev) / 16); ++k) raw[k] = src[k];
+  __builtin_memcpy(&J, raw, sizeof(JobDev));
 }
 
+struct StripIn {
+  u32x2 w[8];   // FP8 bytes: group g = 4*mb + v -> row 16*mb + 4*(lane/16) + v
+  float s[8];   // per-row scales of those rows
+};
+
+__device__ __forceinline__ void load_strip(const JobDev& J, int64_t r0, int64_t c, int lane, StripIn& x) {
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    const int64_t r = r0 + 16 * (g >> 2) + 4 * (lane >> 4) + (g & 3);
+    x.w[g] = (u32x2){0u, 0u};
+    x.s[g] = 1.0f;
+    if (r < J.rows && c < J.cols) {
+      x.w[g] = __builtin_nontemporal_load(G(reinterpret_cast<const u32x2*>(J.w + r * J.cols + c)));
+      if (J.scale_mode == 2) x.s[g] = G(J.scales)[r];
+    }
+  }
+}
+
+// Stage rows [0, pad_rank(rank)) of LoRA A (zero past `rank`), columns
+// [i0, i0 + 128) (zero past `cols`), transposed into AT[slot][koff + k] with
+// slot = (i % 8) * 16 + i / 8 for local column i.
+__device__ __forceinline__ void stage_at(uint16_t* AT, int ld, int koff, const LoraDev& L, int64_t i0,
+                                         int64_t cols, int tid) {
+  const int pairs = pad_rank(L.rank) / 2;
+  const int items = pairs * 16;  // rank pairs x column chunks of 8
+  for (int item = tid; item < items; item += 256) {
+    const int q = item % pairs, cc = item / pairs;
+    const int k = 2 * q;
+    const int64_t col = i0 + 8 * cc;
+    u32x4 lo = (u32x4){0u, 0u, 0u, 0u}, hi = lo;
+    if (col < cols) {
+      if (k < L.rank) lo = *G(reinterpret_cast<const u32x4*>(L.a + (int64_t)k * cols + col));
+      if (k + 1 < L.rank) hi = *G(reinterpret_cast<const u32x4*>(L.a + (int64_t)(k + 1) * cols + col));
+    }
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const uint32_t a0 = (lo[jj >> 1] >> (16 * (jj & 1))) & 0xFFFFu;
+      const uint32_t a1 = (hi[jj >> 1] >> (16 * (jj & 1))) & 0xFFFFu;
+      *reinterpret_cast<uint32_t*>(&AT[(jj * 16 + cc) * ld + koff + k]) = a0 | (a1 << 16);
+    }
+  }
+}
+
+// acc[mb][nb] += (B rows r0 + 16*mb + ..) x (AT slots of N-block nb) over the
+// LoRA's K range; optionally starts the next strip's loads after the first
+// B fragments are in flight.
+__device__ __forceinline__ void lora_mfma(f32x4 (&acc)[2][8], const uint16_t* AT, int ld, int koff,
+                                          const LoraDev& L, int64_t r0, int64_t rows, int ln, int lg) {
+  const int64_t ob0 = r0 + ln, ob1 = r0 + 16 + ln;  // B rows feeding M-blocks 0 and 1
+  for (int kb = 0; kb < L.rank; kb += 32) {
+    const int kk = kb + 8 * lg;
+    bf16x8 b0 = (bf16x8){}, b1 = (bf16x8){};
+    if (kk < L.rank) {
+      if (ob0 < rows) b0 = *G(reinterpret_cast<const bf16x8*>(L.b + ob0 * L.rank + kk));
+      if (ob1 < rows) b1 = *G(reinterpret_cast<const bf16x8*>(L.b + ob1 * L.rank + kk));
+    }
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+      const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + koff + kk]);
+      acc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b0, at, acc[0][nb], 0, 0, 0);
+      acc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b1, at, acc[1][nb], 0, 0, 0);
+    }
+  }
+}
+
+// MULTI = false: exactly one LoRA. MULTI = true: 2..kMaxLoras LoRAs.
 template <bool F32OUT, bool MULTI>
-__global__ __launch_bounds__(256) void k_fused(JobTable tab) {
-  __shared__ __attribute__((aligned(16))) uint16_t AT[kTileN * kATLd];
-  __shared__ __attribute__((aligned(16))) float ACC[4][16 * kAccLd];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MULTI ? 2 : 3))) void k_fused(JobTable tab) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const uint64_t tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int ln = lane & 15;   // MFMA column n / output column group
+  const int lg = lane >> 4;   // MFMA row group (rows 4*lg .. 4*lg+3 of an M-block)
+  const uint64_t unit = xcd_remap(blockIdx.x, gridDim.x);
 
   JobDev J;
-  load_job(tab, tile, J);
-  const uint64_t t = tile - (uint64_t)J.tile_begin;
-  const int64_t o0 = (int64_t)(t / (uint64_t)J.tiles_n) * kTileM;
-  const int64_t i0 = (int64_t)(t % (uint64_t)J.tiles_n) * kTileN;
+  load_job(tab, unit, J);
+  const uint64_t u = unit - (uint64_t)J.unit_begin;
+  const int S = tab.strips;
+  const int64_t i0 = (int64_t)(u % (uint64_t)J.bands_n) * kBandCols;
+  const int64_t row_base = (int64_t)(u / (uint64_t)J.bands_n) * (kWavesPerGroup * S * kStripRows);
   const int64_t rows = J.rows, cols = J.cols;
-  const int fmt = J.fmt;
+  const int64_t ecol = i0 + 8 * ln;
+  const int ld = tab.lds_ld;
+  const int nl = MULTI ? J.n_loras : 1;
 
-  // --- Prefetch this lane's FP8 bytes for the epilogue (8 groups of 8).
-  // Group (h, p): row 32*wave + 16*h + 4*p + lane/16, columns 8*(lane%16)..+7.
-  const int ecol = 8 * (lane & 15);
-  u32x2 raw[8];
-  float rscale[8];
+  // Start the first strip's FP8 stream before anything else.
+  StripIn cur, nxt;
+  load_strip(J, row_base + wave * kStripRows, ecol, lane, cur);
+  const float tscale = J.scale_mode == 1 ? G(J.scales)[0] : 1.0f;
+
+  int koff[kMaxLoras];
+  {
+    int k0 = 0;
 #pragma unroll
-  for (int g = 0; g < 8; ++g) {
-    int64_t r = o0 + 32 * wave + 16 * (g >> 2) + 4 * (g & 3) + (lane >> 4);
-    int64_t c = i0 + ecol;
-    raw[g] = (u32x2){0u, 0u};
-    rscale[g] = 1.0f;
-    if (r < rows && c < cols) {
-      raw[g] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(J.w + r * cols + c));
-      if (J.scale_mode == 2) rscale[g] = J.scales[r];
+    for (int l = 0; l < kMaxLoras; ++l) {
+      koff[l] = k0;
+      if (l < nl) k0 += pad_rank(J.lora[l].rank);
     }
   }
-  const float tscale = J.scale_mode == 1 ? J.scales[0] : 1.0f;
+#pragma unroll
+  for (int l = 0; l < (MULTI ? kMaxLoras : 1); ++l) {
+    if (l >= nl) break;
+    stage_at(AT, ld, koff[l], J.lora[l], i0, cols, tid);
+  }
+  __syncthreads();
 
-  // --- LoRA products.
-  f32x16 acc[4];
-  f32x16 delta[MULTI ? 4 : 1];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) acc[mb] = (f32x16){};
-  float cfin = 0.0f;
+  for (int s = 0; s < S; ++s) {
+    const int64_t r0 = row_base + (int64_t)(s * kWavesPerGroup + wave) * kStripRows;
+    if (r0 >= rows) break;
+    const int64_t r0n = r0 + kWavesPerGroup * kStripRows;
+    const bool more = s + 1 < S && r0n < rows;
 
-  const int64_t orow_b = o0 + 32 * wave + (lane & 31);  // B row this lane feeds
-  const int khalf = 8 * (lane >> 5);
-
+    f32x4 acc[2][8];
+    float cfin;
+    if (!MULTI) {
 #pragma unroll
-  for (int l = 0; l < kMaxLoras; ++l) {
-    if (l >= J.n_loras) break;
-    const LoraDev L = J.lora[l];
-    for (int kc = 0; kc < L.rank; kc += kKC) {
-      __syncthreads();  // previous AT contents fully consumed
-      // Stage A_lora[kc..kc+64) x [i0..i0+128) into AT[i][k], zero outside.
+      for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int it = 0; it < 2; ++it) {
-        int item = tid + 256 * it;  // 32 rank pairs x 16 column chunks of 8
-        int q = item & 31, cc = item >> 5;
-        int k0 = kc + 2 * q;
-        int64_t col = i0 + 8 * cc;
-        u32x4 lo = (u32x4){0u, 0u, 0u, 0u}, hi = lo;
-        if (col < cols) {
-          if (k0 < L.rank) lo = *reinterpret_cast<const u32x4*>(L.a + (int64_t)k0 * cols + col);
-          if (k0 + 1 < L.rank) hi = *reinterpret_cast<const u32x4*>(L.a + (int64_t)(k0 + 1) * cols + col);
-        }
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          uint32_t a0 = (lo[jj >> 1] >> (16 * (jj & 1))) & 0xFFFFu;
-          uint32_t a1 = (hi[jj >> 1] >> (16 * (jj & 1))) & 0xFFFFu;
-          *reinterpret_cast<uint32_t*>(&AT[(8 * cc + jj) * kATLd + 2 * q]) = a0 | (a1 << 16);
-        }
-      }
-      __syncthreads();
-      bf16x8 bfrag[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        int kk = kc + 16 * ks + khalf;
-        bfrag[ks] = (bf16x8){};
-        if (orow_b < rows && kk < L.rank)
-          bfrag[ks] = *reinterpret_cast<const bf16x8*>(L.b + orow_b * L.rank + kk);
-      }
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          bf16x8 afrag = *reinterpret_cast<const bf16x8*>(&AT[(mb * 32 + (lane & 31)) * kATLd + 16 * ks + khalf]);
-          acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afrag, bfrag[ks], acc[mb], 0, 0, 0);
-        }
-      }
-    }
-    if (MULTI) {
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v)
-          delta[mb][v] = l == 0 ? L.coeff * acc[mb][v] : __builtin_fmaf(L.coeff, acc[mb][v], delta[mb][v]);
-        acc[mb] = (f32x16){};
-      }
+        for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      if (more) load_strip(J, r0n, ecol, lane, nxt);
+      lora_mfma(acc, AT, ld, koff[0], J.lora[0], r0, rows, ln, lg);
+      cfin = J.lora[0].coeff;
     } else {
-      cfin = L.coeff;
-    }
-  }
-  if (MULTI) {
+      f32x4 delta[2][8];
+      if (more) load_strip(J, r0n, ecol, lane, nxt);
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) acc[mb] = delta[mb];
-    cfin = 1.0f;
-  }
-  const bool has_lora = J.n_loras > 0;
+      for (int l = 0; l < kMaxLoras; ++l) {
+        if (l >= nl) break;
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        lora_mfma(acc, AT, ld, koff[l], J.lora[l], r0, rows, ln, lg);
+        const float c = J.lora[l].coeff;
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              delta[mb][nb][v] = l == 0 ? c * acc[mb][nb][v] : __builtin_fmaf(c, acc[mb][nb][v], delta[mb][nb][v]);
+      }
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = delta[mb][nb];
+      cfin = 1.0f;
+    }
 
-  // --- Epilogue, 16 rows of each wave's 32 at a time.
-  float* acc_lds = ACC[wave];
+    // --- Epilogue straight from registers.
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    __syncthreads();
-    if (((lane & 31) >> 4) == h) {
-      int orow = (lane & 31) - 16 * h;
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          int icol = mb * 32 + g4 * 8 + 4 * (lane >> 5);
-          *reinterpret_cast<f32x4*>(&acc_lds[orow * kAccLd + icol]) =
-              (f32x4){acc[mb][4 * g4], acc[mb][4 * g4 + 1], acc[mb][4 * g4 + 2], acc[mb][4 * g4 + 3]};
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int g = 4 * h + p;
-      const int orow = 4 * p + (lane >> 4);
-      const int64_t r = o0 + 32 * wave + 16 * h + orow;
-      const int64_t c = i0 + ecol;
-      if (r < rows && c < cols) {
-        f32x4 d0 = *reinterpret_cast<const f32x4*>(&acc_lds[orow * kAccLd + ecol]);
-        f32x4 d1 = *reinterpret_cast<const f32x4*>(&acc_lds[orow * kAccLd + ecol + 4]);
-        float v[8];
-        decode4(raw[g][0], fmt, v);
-        decode4(raw[g][1], fmt, v + 4);
-        const float s = J.scale_mode == 2 ? rscale[g] : tscale;
-        float d[8] = {d0[0], d0[1], d0[2], d0[3], d1[0], d1[1], d1[2], d1[3]};
+    for (int g = 0; g < 8; ++g) {
+      const int mb = g >> 2, v = g & 3;
+      const int64_t r = r0 + 16 * mb + 4 * lg + v;
+      if (r < rows && ecol < cols) {
+        float x[8];
+        decode4(cur.w[g][0], J.fmt, x);
+        decode4(cur.w[g][1], J.fmt, x + 4);
+        const float sc = J.scale_mode == 2 ? cur.s[g] : tscale;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          if (J.scale_mode != 0) v[j] = __builtin_fmaf(s, v[j], 0.0f);
-          if (has_lora) v[j] = __builtin_fmaf(cfin, d[j], v[j]);
-          v[j] = canon_nan(v[j]);
+          if (J.scale_mode != 0) x[j] = __builtin_fmaf(sc, x[j], 0.0f);
+          x[j] = canon_nan(__builtin_fmaf(cfin, acc[mb][j][v], x[j]));
         }
         if (F32OUT) {
-          f32x4* dst = reinterpret_cast<f32x4*>(reinterpret_cast<float*>(J.out) + r * cols + c);
-          __builtin_nontemporal_store((f32x4){v[0], v[1], v[2], v[3]}, dst);
-          __builtin_nontemporal_store((f32x4){v[4], v[5], v[6], v[7]}, dst + 1);
+          auto dst = G(reinterpret_cast<f32x4*>(reinterpret_cast<float*>(J.out) + r * cols + ecol));
+          __builtin_nontemporal_store((f32x4){x[0], x[1], x[2], x[3]}, dst);
+          __builtin_nontemporal_store((f32x4){x[4], x[5], x[6], x[7]}, dst + 1);
         } else {
-          u32x4 o = {pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7])};
-          __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(J.out) + r * cols + c));
+          const u32x4 o = {pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]), pack_bf16(x[4], x[5]), pack_bf16(x[6], x[7])};
+          __builtin_nontemporal_store(o, G(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(J.out) + r * cols + ecol)));
         }
       }
     }
+    cur = nxt;
   }
 }
 
@@ -381,14 +417,15 @@ hipError_t launch_dequant(const DequantArgs& a, int fmt, int scale_mode, bool f3
 }
 
 hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, hipStream_t stream) {
-  if (t.total_tiles == 0) return hipSuccess;
-  dim3 grid((unsigned)t.total_tiles);
+  if (t.total_units == 0) return hipSuccess;
+  dim3 grid((unsigned)t.total_units);
+  size_t lds = (size_t)kBandCols * (size_t)t.lds_ld * sizeof(uint16_t);
   if (f32out) {
-    if (multi) hipLaunchKernelGGL((k_fused<true, true>), grid, dim3(256), 0, stream, t);
-    else hipLaunchKernelGGL((k_fused<true, false>), grid, dim3(256), 0, stream, t);
+    if (multi) hipLaunchKernelGGL((k_fused<true, true>), grid, dim3(256), lds, stream, t);
+    else hipLaunchKernelGGL((k_fused<true, false>), grid, dim3(256), lds, stream, t);
   } else {
-    if (multi) hipLaunchKernelGGL((k_fused<false, true>), grid, dim3(256), 0, stream, t);
-    else hipLaunchKernelGGL((k_fused<false, false>), grid, dim3(256), 0, stream, t);
+    if (multi) hipLaunchKernelGGL((k_fused<false, true>), grid, dim3(256), lds, stream, t);
+    else hipLaunchKernelGGL((k_fused<false, false>), grid, dim3(256), lds, stream, t);
   }
   return hipGetLastError();
 }

@@ -224,6 +224,31 @@ def test_invalid_arguments_report_status(ctx):
         ctx.free(p)
 
 
+def test_undersized_buffers_rejected_before_launch(ctx):
+    """A buffer smaller than the tensor it is passed for is an InvalidArgument
+    (checked on the host against the allocation's extent), never a launch."""
+    log("case: undersized buffers")
+    small, big = ctx.alloc(1024), ctx.alloc(1 << 20)
+    try:
+        E4, NONE, ROW = lw.FMT_E4M3FN, lw.SCALE_NONE, lw.SCALE_ROW
+        with pytest.raises(lw.InvalidArgument, match="weight"):
+            ctx.dequant(small, 64, 64, E4, NONE, None, big)
+        with pytest.raises(lw.InvalidArgument, match="output"):
+            ctx.dequant(big, 64, 64, E4, NONE, None, small)
+        with pytest.raises(lw.InvalidArgument, match="scales"):
+            ctx.dequant(big, 512, 64, E4, ROW, small, big)
+        with pytest.raises(lw.InvalidArgument, match="LoRA B"):
+            ctx.dequant_lora(big, 64, 64, E4, NONE, None, [(small, big, 64, 1.0)], big)
+        with pytest.raises(lw.InvalidArgument, match="LoRA A"):
+            ctx.dequant_lora(big, 64, 64, E4, NONE, None, [(big, small, 64, 1.0)], big)
+        with pytest.raises(lw.InvalidArgument, match="weight"):
+            ctx.dequant(big + (1 << 20) - 100, 1, 200, E4, NONE, None, big)
+        ctx.synchronize()
+    finally:
+        ctx.free(small)
+        ctx.free(big)
+
+
 def test_upload_download_round_trip(ctx):
     log("case: round trip")
     rng = np.random.default_rng(1)
