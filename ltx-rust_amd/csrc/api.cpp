@@ -29,11 +29,16 @@ struct ltxw_ctx {
   std::vector<hipEvent_t> stage_done;
   size_t stage_bytes = 0;
   size_t next_stage = 0;
-  // Job tables of grouped launches: pinned host mirror -> device buffer.
-  void* table_host = nullptr;
-  void* table_dev = nullptr;
-  size_t table_cap = 0;
-  hipEvent_t table_done = nullptr;
+  // Job tables of grouped launches: a ring of pinned host mirrors -> device
+  // buffers, so that the host can queue several launches ahead of the GPU.
+  struct TableSlot {
+    void* host = nullptr;
+    void* dev = nullptr;
+    size_t cap = 0;
+    hipEvent_t copied = nullptr;  // recorded after the slot's last upload
+  };
+  std::vector<TableSlot> tables;
+  size_t next_table = 0;
   std::string err;
 };
 
@@ -147,10 +152,15 @@ ltxw::JobDev to_job(const ltxw_tensor_desc& d) {
 // The tiled MFMA kernel's layout requirements (else: generic kernel).
 bool fused_ok(const ltxw_tensor_desc& d) {
   if (d.cols % 8 != 0 || !aligned(d.w, 16) || !aligned(d.out, 16)) return false;
-  if ((d.cols + ltxw::kBandCols - 1) / ltxw::kBandCols > INT32_MAX) return false;
+  if (d.scale_mode == LTXW_SCALE_ROW && !aligned(d.scales, 16)) return false;  // read 4 rows at a time
+  // The kernel addresses every buffer with 32-bit byte offsets.
+  const uint64_t lim = UINT32_MAX - 64;
+  if ((uint64_t)d.rows * (uint64_t)d.cols * 4 > lim) return false;
   int k = 0;
   for (int l = 0; l < d.n_loras; ++l) {
-    if (d.loras[l].rank % 8 != 0 || !aligned(d.loras[l].a, 16) || !aligned(d.loras[l].b, 16)) return false;
+    const uint64_t r = (uint64_t)d.loras[l].rank;
+    if (r % 8 != 0 || !aligned(d.loras[l].a, 16) || !aligned(d.loras[l].b, 16)) return false;
+    if (2 * r * (uint64_t)d.rows > lim || 2 * r * (uint64_t)d.cols > lim) return false;
     k += ltxw::pad_rank(d.loras[l].rank);
   }
   return k <= ltxw::kRankMax;
@@ -178,23 +188,26 @@ int run_dequant(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t n) {
   return LTXW_OK;
 }
 
-// Grows the grouped-launch job table (pinned host + device) to `bytes`.
-int ensure_table(ltxw_ctx* ctx, size_t bytes) {
-  if (bytes <= ctx->table_cap) {
-    HIP_TRY(ctx, hipEventSynchronize(ctx->table_done), "job table wait");
-    return LTXW_OK;
+// Next job-table slot with room for `bytes`. Its host mirror is reusable once
+// the slot's previous upload has completed; the device copy is ordered on the
+// compute stream after every earlier kernel that read it.
+int take_table(ltxw_ctx* ctx, size_t bytes, ltxw_ctx::TableSlot** out) {
+  ltxw_ctx::TableSlot& t = ctx->tables[ctx->next_table];
+  ctx->next_table = (ctx->next_table + 1) % ctx->tables.size();
+  HIP_TRY(ctx, hipEventSynchronize(t.copied), "job table wait");
+  if (bytes > t.cap) {
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->compute), "job table resize");
+    if (t.host) (void)hipHostFree(t.host);
+    if (t.dev) (void)hipFree(t.dev);
+    t.host = t.dev = nullptr;
+    t.cap = 0;
+    size_t cap = std::max<size_t>(bytes, 64 * 1024);
+    if (hipHostMalloc(&t.host, cap, hipHostMallocDefault) != hipSuccess)
+      return fail(ctx, LTXW_ERR_OOM, "pinned job table of %zu bytes", cap);
+    if (hipMalloc(&t.dev, cap) != hipSuccess) return fail(ctx, LTXW_ERR_OOM, "device job table of %zu bytes", cap);
+    t.cap = cap;
   }
-  HIP_TRY(ctx, hipStreamSynchronize(ctx->compute), "job table resize");
-  if (ctx->table_host) (void)hipHostFree(ctx->table_host);
-  if (ctx->table_dev) (void)hipFree(ctx->table_dev);
-  ctx->table_host = ctx->table_dev = nullptr;
-  ctx->table_cap = 0;
-  size_t cap = std::max<size_t>(bytes, 64 * 1024);
-  if (hipHostMalloc(&ctx->table_host, cap, hipHostMallocDefault) != hipSuccess)
-    return fail(ctx, LTXW_ERR_OOM, "pinned job table of %zu bytes", cap);
-  if (hipMalloc(&ctx->table_dev, cap) != hipSuccess)
-    return fail(ctx, LTXW_ERR_OOM, "device job table of %zu bytes", cap);
-  ctx->table_cap = cap;
+  *out = &t;
   return LTXW_OK;
 }
 
@@ -205,21 +218,13 @@ int job_k(const ltxw::JobDev& j) {
   return k;
 }
 
-// One fused launch over `jobs` (all fused_ok, same out dtype and multi flag).
-// Strips per wave S: enough that every CU keeps about two workgroups busy
-// for the whole launch (fewer, longer-lived waves that prefetch ahead).
+// One fused launch over `jobs` (all fused_ok, same out dtype and multi flag):
+// one workgroup per 128 x 128 output tile of every job.
 int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool multi) {
   if (jobs.empty()) return LTXW_OK;
-  int64_t strips = 0;
   int kmax = 0;
-  for (auto& j : jobs) {
-    strips += (int64_t)j.bands_n * ((j.rows + ltxw::kStripRows - 1) / ltxw::kStripRows);
-    kmax = std::max(kmax, job_k(j));
-  }
-  const int64_t target_waves = (int64_t)ctx->cu_count * 2 * ltxw::kWavesPerGroup;
-  int64_t S = std::max<int64_t>(1, (strips + target_waves - 1) / target_waves);
-  S = std::min<int64_t>(S, 1 << 20);
-  const int64_t group_rows = (int64_t)ltxw::kWavesPerGroup * S * ltxw::kStripRows;
+  for (auto& j : jobs) kmax = std::max(kmax, job_k(j));
+  const int64_t group_rows = (int64_t)ltxw::kWavesPerGroup * ltxw::kStripRows;
   int64_t units = 0;
   for (auto& j : jobs) {
     j.unit_begin = units;
@@ -228,7 +233,6 @@ int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool 
   if (units > INT32_MAX) return fail(ctx, LTXW_ERR_INVALID_ARG, "launch of %lld work units is too large", (long long)units);
   ltxw::JobTable t{};
   t.n_jobs = (int32_t)jobs.size();
-  t.strips = (int32_t)S;
   t.total_units = units;
   t.lds_ld = kmax + 8;
   if (jobs.size() == 1) {
@@ -237,16 +241,17 @@ int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool 
     size_t jb = jobs.size() * sizeof(ltxw::JobDev);
     size_t bb = jobs.size() * sizeof(int64_t);
     size_t off_b = (jb + 255) & ~size_t(255);
-    int rc = ensure_table(ctx, off_b + bb);
+    ltxw_ctx::TableSlot* slot = nullptr;
+    int rc = take_table(ctx, off_b + bb, &slot);
     if (rc) return rc;
-    memcpy(ctx->table_host, jobs.data(), jb);
-    int64_t* begins = reinterpret_cast<int64_t*>((char*)ctx->table_host + off_b);
+    memcpy(slot->host, jobs.data(), jb);
+    int64_t* begins = reinterpret_cast<int64_t*>((char*)slot->host + off_b);
     for (size_t k = 0; k < jobs.size(); ++k) begins[k] = jobs[k].unit_begin;
-    HIP_TRY(ctx, hipMemcpyAsync(ctx->table_dev, ctx->table_host, off_b + bb, hipMemcpyHostToDevice, ctx->compute),
+    HIP_TRY(ctx, hipMemcpyAsync(slot->dev, slot->host, off_b + bb, hipMemcpyHostToDevice, ctx->compute),
             "job table upload");
-    HIP_TRY(ctx, hipEventRecord(ctx->table_done, ctx->compute), "job table event");
-    t.jobs = reinterpret_cast<const ltxw::JobDev*>(ctx->table_dev);
-    t.begins = reinterpret_cast<const int64_t*>((char*)ctx->table_dev + off_b);
+    HIP_TRY(ctx, hipEventRecord(slot->copied, ctx->compute), "job table event");
+    t.jobs = reinterpret_cast<const ltxw::JobDev*>(slot->dev);
+    t.begins = reinterpret_cast<const int64_t*>((char*)slot->dev + off_b);
   }
   HIP_TRY(ctx, ltxw::launch_fused(t, f32out, multi, ctx->compute), "fused kernel launch");
   return LTXW_OK;
@@ -313,8 +318,10 @@ int ltxw_ctx_create(int device, size_t staging_bytes, int n_staging, ltxw_ctx** 
     return bail(LTXW_ERR_HIP, "compute stream", e);
   if ((e = hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking)) != hipSuccess)
     return bail(LTXW_ERR_HIP, "copy stream", e);
-  if ((e = hipEventCreateWithFlags(&c->table_done, hipEventDisableTiming)) != hipSuccess)
-    return bail(LTXW_ERR_HIP, "event", e);
+  c->tables.resize(16);
+  for (auto& t : c->tables)
+    if ((e = hipEventCreateWithFlags(&t.copied, hipEventDisableTiming)) != hipSuccess)
+      return bail(LTXW_ERR_HIP, "event", e);
   for (int k = 0; k < n_staging; ++k) {
     void* p = nullptr;
     hipEvent_t ev = nullptr;
@@ -336,9 +343,11 @@ void ltxw_ctx_destroy(ltxw_ctx* ctx) {
   if (ctx->copy) (void)hipStreamSynchronize(ctx->copy);
   for (void* p : ctx->stage) (void)hipHostFree(p);
   for (hipEvent_t ev : ctx->stage_done) (void)hipEventDestroy(ev);
-  if (ctx->table_host) (void)hipHostFree(ctx->table_host);
-  if (ctx->table_dev) (void)hipFree(ctx->table_dev);
-  if (ctx->table_done) (void)hipEventDestroy(ctx->table_done);
+  for (auto& t : ctx->tables) {
+    if (t.host) (void)hipHostFree(t.host);
+    if (t.dev) (void)hipFree(t.dev);
+    if (t.copied) (void)hipEventDestroy(t.copied);
+  }
   if (ctx->compute) (void)hipStreamDestroy(ctx->compute);
   if (ctx->copy) (void)hipStreamDestroy(ctx->copy);
   delete ctx;

@@ -9,9 +9,8 @@ namespace ltxw {
 constexpr int kMaxLoras = 4;
 
 // Work decomposition of the fused kernel. A workgroup (4 waves) owns one
-// band of kBandCols output columns and a group of 4 * S strips of kStripRows
-// rows each (S = strips per wave, chosen per launch); wave w takes strips
-// w, w + 4, w + 8, ...
+// band of kBandCols output columns and 4 strips of kStripRows rows; wave w
+// takes strip w.
 constexpr int kBandCols = 128;
 constexpr int kStripRows = 32;
 constexpr int kWavesPerGroup = 4;
@@ -46,9 +45,8 @@ struct JobTable {
   const JobDev* jobs;    // device array when n_jobs > 1
   const int64_t* begins; // device array of unit_begin, ascending
   int32_t n_jobs;
-  int32_t strips;        // S: strips per wave
   int64_t total_units;   // workgroups in the launch
-  int32_t lds_ld;        // AT row stride (bf16) sized for the launch's largest rank
+  int32_t lds_ld;        // AT row stride (bf16): 8 + the launch's largest total padded rank
 };
 
 struct DequantArgs {

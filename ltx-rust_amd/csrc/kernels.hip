@@ -27,6 +27,20 @@ __device__ __forceinline__ float canon_nan(float x) {
   return __builtin_isnan(x) ? __builtin_bit_cast(float, kCanonNaN) : x;
 }
 
+// Canonicalise the NaNs among n values, paying only a compare per value when
+// the whole wave holds none (the usual case): the per-value NaN tests are
+// combined into one wave-wide mask, and the selects run only if it is set.
+template <int N>
+__device__ __forceinline__ void canon_nan_wave(float* v) {
+  uint64_t any = 0;
+#pragma unroll
+  for (int j = 0; j < N; ++j) any |= __builtin_amdgcn_ballot_w64(__builtin_isnan(v[j]));
+  if (any) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = canon_nan(v[j]);
+  }
+}
+
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   bf16x2 r = __builtin_convertvector((f32x2){a, b}, bf16x2);
   return __builtin_bit_cast(uint32_t, r);
@@ -79,6 +93,8 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t n) {
 // ---------------------------------------------------------------------------
 // (a) Streaming dequant. Each thread handles kChunksPerThread chunks of 16
 // FP8 bytes: one 128-bit load, two 128-bit bf16 stores (four for f32).
+// Loads are non-temporal (read once); stores are ordinary, which measured
+// faster than non-temporal stores for this kernel on MI355X.
 // ---------------------------------------------------------------------------
 constexpr int kChunksPerThread = 4;
 
@@ -115,19 +131,17 @@ __global__ __launch_bounds__(256) void k_dequant(DequantArgs a) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) v[j] = __builtin_fmaf((uint64_t)j < edge ? s0 : s1, v[j], 0.0f);
     }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = canon_nan(v[j]);
+    canon_nan_wave<16>(v);
     if (F32OUT) {
       f32x4* dst = reinterpret_cast<f32x4*>(a.out) + idx * 4;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        __builtin_nontemporal_store((f32x4){v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]}, dst + q);
+      for (int q = 0; q < 4; ++q) G(dst)[q] = (f32x4){v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
     } else {
       u32x4* dst = reinterpret_cast<u32x4*>(a.out) + idx * 2;
       u32x4 lo = {pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7])};
       u32x4 hi = {pack_bf16(v[8], v[9]), pack_bf16(v[10], v[11]), pack_bf16(v[12], v[13]), pack_bf16(v[14], v[15])};
-      __builtin_nontemporal_store(lo, dst);
-      __builtin_nontemporal_store(hi, dst + 1);
+      G(dst)[0] = lo;
+      G(dst)[1] = hi;
     }
   }
 }
@@ -169,8 +183,8 @@ __global__ __launch_bounds__(256) void k_generic(GenericArgs g) {
 // ---------------------------------------------------------------------------
 // (b) Fused dequant + LoRA merge.
 //
-// Workgroup: 4 waves. Work unit: one band of 128 output columns [i0, i0+128)
-// and 4*S strips of 32 rows; wave w walks strips w, w+4, ... of the unit.
+// Workgroup: 4 waves; work unit: one band of 128 output columns [i0, i0+128)
+// by 128 rows; wave w owns the strip of rows [r0, r0+32), r0 = 128*g + 32*w.
 //
 // LoRA product on v_mfma_f32_16x16x32_bf16 with M = output row o, N = output
 // column i, K = rank r, and the N index permuted as i = i0 + 8*n + nb for
@@ -178,14 +192,18 @@ __global__ __launch_bounds__(256) void k_generic(GenericArgs g) {
 // column n = l%16 and rows m = 4*(l/16) + v), lane l then owns, for each of
 // its 8 rows, the 8 contiguous columns i0 + 8*(l%16) .. +7 across the 8
 // N-blocks: the FP8 input (8 bytes per lane) and the bf16 output (16 bytes per
-// lane) are read and written straight from registers, 16 lanes covering 128
+// lane) go straight between registers and HBM, 16 lanes covering 128
 // contiguous columns of a row, with no LDS relayout.
 //   A operand (o x r): LoRA B rows, 16-byte loads (r contiguous), from L2.
-//   B operand (r x i): LoRA A transposed, staged once per work unit in LDS as
+//   B operand (r x i): LoRA A transposed, staged per work unit in LDS as
 //                      AT[slot][k] with slot = nb*16 + n (consecutive lanes
 //                      read consecutive slots: conflict-free 128-bit reads).
 // Several LoRAs are staged side by side along k (each padded to 32).
-// The FP8 bytes of the next strip are loaded while the current one computes.
+//
+// Issue order is latency order: the L2-resident factor loads (A for the LDS
+// stage, then every B fragment) go out first, the FP8 bytes and scales from
+// HBM last. Loads retire in order, so staging, the barrier and the MFMAs run
+// while the HBM data is still in flight.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void load_job(const JobTable& t, uint64_t unit, JobDev& J) {
   if (t.n_jobs == 1) {
@@ -206,184 +224,263 @@ __device__ __forceinline__ void load_job(const JobTable& t, uint64_t unit, JobDe
   __builtin_memcpy(&J, raw, sizeof(JobDev));
 }
 
-struct StripIn {
-  u32x2 w[8];   // FP8 bytes: group g = 4*mb + v -> row 16*mb + 4*(lane/16) + v
-  float s[8];   // per-row scales of those rows
+// K-steps (32 ranks each) of all of a tensor's LoRAs, side by side: LoRA l
+// owns K-steps [kst_l, kst_l + pad_rank(rank_l) / 32). For K-step t of LoRA l
+// (local step kt = t - kst_l), thread tid stages ranks 32*kt + 2*(tid % 16)
+// and +1 of A for the 8 columns i0 + 8*(tid / 16) .. +7 into
+// AT[slot][32*t + ..] with slot = (i % 8) * 16 + i / 8 for local column i.
+struct LoraSteps {
+  int kst[kMaxLoras];   // first K-step of each LoRA
+  int nks[kMaxLoras];   // K-steps of each LoRA
+  int total;            // sum of nks
 };
 
-__device__ __forceinline__ void load_strip(const JobDev& J, int64_t r0, int64_t c, int lane, StripIn& x) {
+// Owner LoRA of K-step t, the step's index within that LoRA, and whether it
+// is the LoRA's last step (static loop: no run-time indexing of arrays).
+struct StepInfo {
+  int l;
+  int kt;
+  bool last;
+};
+
+__device__ __forceinline__ StepInfo step_info(const LoraSteps& S, int t) {
+  StepInfo r{0, t, false};
+#pragma unroll
+  for (int q = 0; q < kMaxLoras; ++q) {
+    if (S.nks[q] > 0 && t >= S.kst[q] && t < S.kst[q] + S.nks[q]) {
+      r.l = q;
+      r.kt = t - S.kst[q];
+      r.last = t == S.kst[q] + S.nks[q] - 1;
+    }
+  }
+  return r;
+}
+
+// Loads and stores at a 32-bit byte offset from a wave-uniform base pointer,
+// so the compiler can use the SGPR-base + VGPR-offset addressing mode (one
+// VGPR of address per lane, no 64-bit address arithmetic). The host routes
+// tensors whose byte extents do not fit 32 bits to the generic kernel.
+template <typename T>
+__device__ __forceinline__ T ld_at(const void* base, uint32_t off) {
+  return *reinterpret_cast<const __attribute__((address_space(1))) T*>(
+      (const __attribute__((address_space(1))) char*)base + off);
+}
+template <typename T>
+__device__ __forceinline__ T ld_nt_at(const void* base, uint32_t off) {
+  return __builtin_nontemporal_load(reinterpret_cast<const __attribute__((address_space(1))) T*>(
+      (const __attribute__((address_space(1))) char*)base + off));
+}
+template <typename T>
+__device__ __forceinline__ void st_nt_at(void* base, uint32_t off, T v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<__attribute__((address_space(1))) T*>(
+                                     (__attribute__((address_space(1))) char*)base + off));
+}
+
+// One work unit: rows [g0, g0 + 128) x columns [i0, i0 + 128) of job J.
+// FULL: the unit lies entirely inside the tensor (no bounds tests).
+// FMT: 0 = e4m3fn, 1 = e5m2 (J.fmt, resolved once per workgroup).
+template <bool F32OUT, bool MULTI, int KS, bool FULL, int FMT>
+__device__ __forceinline__ void fused_unit(const JobDev& J, const LoraSteps& LS, uint16_t* AT, int ld,
+                                           uint32_t i0, uint32_t g0, int tid) {
+  const int lane = tid & 63, wave = tid >> 6;
+  const int ln = lane & 15;  // MFMA column n / output column group
+  const int lg = lane >> 4;  // MFMA row group (rows 4*lg .. 4*lg+3 of an M-block)
+  const uint32_t rows = (uint32_t)J.rows, cols = (uint32_t)J.cols;
+  const uint32_t r0 = g0 + kStripRows * wave;
+  const uint32_t ecol = i0 + 8 * ln;
+  const bool col_ok = FULL || ecol < cols;
+
+  // 1. L2-resident factors: the A stage of every K-step, then the B fragments.
+  const int sq = tid & 15;
+  const uint32_t scol = i0 + 8 * (tid >> 4);
+  const bool scol_ok = FULL || scol < cols;
+  u32x4 st_lo[KS], st_hi[KS];
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    st_lo[t] = (u32x4){0u, 0u, 0u, 0u};
+    st_hi[t] = st_lo[t];
+    if (t < LS.total) {
+      const StepInfo si = MULTI ? step_info(LS, t) : StepInfo{0, t, false};
+      const uint32_t k = 32 * si.kt + 2 * sq;
+#pragma unroll
+      for (int q = 0; q < (MULTI ? kMaxLoras : 1); ++q) {
+        if (si.l != q) continue;  // uniform; keeps J.lora indexed statically
+        const LoraDev& L = J.lora[q];
+        if (scol_ok && k < (uint32_t)L.rank) st_lo[t] = ld_at<u32x4>(L.a, 2 * (k * cols + scol));
+        if (scol_ok && k + 1 < (uint32_t)L.rank) st_hi[t] = ld_at<u32x4>(L.a, 2 * ((k + 1) * cols + scol));
+      }
+    }
+  }
+  bf16x8 bf[KS][2];
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    bf[t][0] = (bf16x8){};
+    bf[t][1] = (bf16x8){};
+    if (t < LS.total) {
+      const StepInfo si = MULTI ? step_info(LS, t) : StepInfo{0, t, false};
+      const uint32_t kk = 32 * si.kt + 8 * lg;
+#pragma unroll
+      for (int q = 0; q < (MULTI ? kMaxLoras : 1); ++q) {
+        if (si.l != q) continue;
+        const LoraDev& L = J.lora[q];
+        const uint32_t rank = (uint32_t)L.rank;
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+          const uint32_t ob = r0 + 16 * mb + ln;
+          if (kk < rank && (FULL || ob < rows)) bf[t][mb] = ld_at<bf16x8>(L.b, 2 * (ob * rank + kk));
+        }
+      }
+    }
+  }
+
+  // 2. HBM: this lane's FP8 bytes (8 rows x 8 columns) and their scales.
+  //    Group g = 4*mb + v is row r0 + 16*mb + 4*lg + v.
+  const uint32_t rl = r0 + 4 * lg;
+  const uint32_t e0 = rl * cols + ecol;  // element offset of group 0
+  u32x2 wv[8];
 #pragma unroll
   for (int g = 0; g < 8; ++g) {
-    const int64_t r = r0 + 16 * (g >> 2) + 4 * (lane >> 4) + (g & 3);
-    x.w[g] = (u32x2){0u, 0u};
-    x.s[g] = 1.0f;
-    if (r < J.rows && c < J.cols) {
-      x.w[g] = __builtin_nontemporal_load(G(reinterpret_cast<const u32x2*>(J.w + r * J.cols + c)));
-      if (J.scale_mode == 2) x.s[g] = G(J.scales)[r];
+    const uint32_t dr = 16 * (g >> 2) + (g & 3);
+    wv[g] = (u32x2){0u, 0u};
+    if (col_ok && (FULL || rl + dr < rows)) wv[g] = ld_nt_at<u32x2>(J.w, e0 + dr * cols);
+  }
+  float sc[8];
+  if (J.scale_mode == 2) {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const uint32_t rb = rl + 16 * mb;
+      if (FULL || rb + 3 < rows) {
+        const f32x4 q = ld_at<f32x4>(J.scales, 4 * rb);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sc[4 * mb + v] = q[v];
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sc[4 * mb + v] = rb + v < rows ? ld_at<float>(J.scales, 4 * (rb + v)) : 1.0f;
+      }
+    }
+  } else {
+    const float t = J.scale_mode == 1 ? ld_at<float>(J.scales, 0) : 1.0f;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) sc[g] = t;
+  }
+
+  // 3. LDS stage, then the MFMAs (their inputs are already in flight).
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    if (t < LS.total) {
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        // (A[k][i], A[k+1][i]) for column i = scol + jj: the same half of word jj/2 of each row.
+        const uint32_t pair = __builtin_amdgcn_perm(st_hi[t][jj >> 1], st_lo[t][jj >> 1],
+                                                    (jj & 1) ? 0x07060302u : 0x05040100u);
+        *reinterpret_cast<uint32_t*>(&AT[(jj * 16 + (tid >> 4)) * ld + 32 * t + 2 * sq]) = pair;
+      }
     }
   }
-}
+  __syncthreads();
 
-// Stage rows [0, pad_rank(rank)) of LoRA A (zero past `rank`), columns
-// [i0, i0 + 128) (zero past `cols`), transposed into AT[slot][koff + k] with
-// slot = (i % 8) * 16 + i / 8 for local column i.
-__device__ __forceinline__ void stage_at(uint16_t* AT, int ld, int koff, const LoraDev& L, int64_t i0,
-                                         int64_t cols, int tid) {
-  const int pairs = pad_rank(L.rank) / 2;
-  const int items = pairs * 16;  // rank pairs x column chunks of 8
-  for (int item = tid; item < items; item += 256) {
-    const int q = item % pairs, cc = item / pairs;
-    const int k = 2 * q;
-    const int64_t col = i0 + 8 * cc;
-    u32x4 lo = (u32x4){0u, 0u, 0u, 0u}, hi = lo;
-    if (col < cols) {
-      if (k < L.rank) lo = *G(reinterpret_cast<const u32x4*>(L.a + (int64_t)k * cols + col));
-      if (k + 1 < L.rank) hi = *G(reinterpret_cast<const u32x4*>(L.a + (int64_t)(k + 1) * cols + col));
-    }
+  f32x4 acc[2][8];
+  f32x4 delta[MULTI ? 2 : 1][MULTI ? 8 : 1];
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      const uint32_t a0 = (lo[jj >> 1] >> (16 * (jj & 1))) & 0xFFFFu;
-      const uint32_t a1 = (hi[jj >> 1] >> (16 * (jj & 1))) & 0xFFFFu;
-      *reinterpret_cast<uint32_t*>(&AT[(jj * 16 + cc) * ld + koff + k]) = a0 | (a1 << 16);
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    if (t < LS.total) {
+      const int kk = 32 * t + 8 * lg;
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) {
+        const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + kk]);
+        acc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[t][0], at, acc[0][nb], 0, 0, 0);
+        acc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[t][1], at, acc[1][nb], 0, 0, 0);
+      }
+      if (MULTI) {
+        // Last K-step of its LoRA: fold coeff * (B A) into the running sum.
+        const StepInfo si = step_info(LS, t);
+        if (si.last) {
+          float c = J.lora[0].coeff;
+#pragma unroll
+          for (int q = 1; q < kMaxLoras; ++q)
+            if (si.l == q) c = J.lora[q].coeff;
+          const bool first = si.l == 0;
+#pragma unroll
+          for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) {
+#pragma unroll
+              for (int v = 0; v < 4; ++v)
+                delta[mb][nb][v] = first ? c * acc[mb][nb][v] : __builtin_fmaf(c, acc[mb][nb][v], delta[mb][nb][v]);
+              acc[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            }
+        }
+      }
     }
   }
-}
-
-// acc[mb][nb] += (B rows r0 + 16*mb + ..) x (AT slots of N-block nb) over the
-// LoRA's K range; optionally starts the next strip's loads after the first
-// B fragments are in flight.
-__device__ __forceinline__ void lora_mfma(f32x4 (&acc)[2][8], const uint16_t* AT, int ld, int koff,
-                                          const LoraDev& L, int64_t r0, int64_t rows, int ln, int lg) {
-  const int64_t ob0 = r0 + ln, ob1 = r0 + 16 + ln;  // B rows feeding M-blocks 0 and 1
-  for (int kb = 0; kb < L.rank; kb += 32) {
-    const int kk = kb + 8 * lg;
-    bf16x8 b0 = (bf16x8){}, b1 = (bf16x8){};
-    if (kk < L.rank) {
-      if (ob0 < rows) b0 = *G(reinterpret_cast<const bf16x8*>(L.b + ob0 * L.rank + kk));
-      if (ob1 < rows) b1 = *G(reinterpret_cast<const bf16x8*>(L.b + ob1 * L.rank + kk));
-    }
+  float cfin = J.lora[0].coeff;
+  if (MULTI) {
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + koff + kk]);
-      acc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b0, at, acc[0][nb], 0, 0, 0);
-      acc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b1, at, acc[1][nb], 0, 0, 0);
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = delta[mb][nb];
+    cfin = 1.0f;
+  }
+
+  // 4. Epilogue straight from registers:
+  //    out = RNE(fma(cfin, delta, fma(scale, decode(w), 0))), scale = 1 when unscaled.
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    const int mb = g >> 2, v = g & 3;
+    const uint32_t dr = 16 * mb + v;
+    if (col_ok && (FULL || rl + dr < rows)) {
+      float x[8];
+      decode4(wv[g][0], FMT, x);
+      decode4(wv[g][1], FMT, x + 4);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = __builtin_fmaf(cfin, acc[mb][j][v], __builtin_fmaf(sc[g], x[j], 0.0f));
+      canon_nan_wave<8>(x);
+      const uint32_t e = e0 + dr * cols;
+      if (F32OUT) {
+        st_nt_at<f32x4>(J.out, 4 * e, (f32x4){x[0], x[1], x[2], x[3]});
+        st_nt_at<f32x4>(J.out, 4 * e + 16, (f32x4){x[4], x[5], x[6], x[7]});
+      } else {
+        const u32x4 o = {pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]), pack_bf16(x[4], x[5]), pack_bf16(x[6], x[7])};
+        st_nt_at<u32x4>(J.out, 2 * e, o);
+      }
     }
   }
 }
 
 // MULTI = false: exactly one LoRA. MULTI = true: 2..kMaxLoras LoRAs.
-template <bool F32OUT, bool MULTI>
+// KS >= total K-steps of every job in the launch (register arrays are sized by it).
+template <bool F32OUT, bool MULTI, int KS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MULTI ? 2 : 3))) void k_fused(JobTable tab) {
   extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int ln = lane & 15;   // MFMA column n / output column group
-  const int lg = lane >> 4;   // MFMA row group (rows 4*lg .. 4*lg+3 of an M-block)
   const uint64_t unit = xcd_remap(blockIdx.x, gridDim.x);
-
   JobDev J;
   load_job(tab, unit, J);
   const uint64_t u = unit - (uint64_t)J.unit_begin;
-  const int S = tab.strips;
-  const int64_t i0 = (int64_t)(u % (uint64_t)J.bands_n) * kBandCols;
-  const int64_t row_base = (int64_t)(u / (uint64_t)J.bands_n) * (kWavesPerGroup * S * kStripRows);
-  const int64_t rows = J.rows, cols = J.cols;
-  const int64_t ecol = i0 + 8 * ln;
-  const int ld = tab.lds_ld;
+  const uint32_t i0 = (uint32_t)(u % (uint64_t)J.bands_n) * kBandCols;
+  const uint32_t g0 = (uint32_t)(u / (uint64_t)J.bands_n) * (kWavesPerGroup * kStripRows);
   const int nl = MULTI ? J.n_loras : 1;
-
-  // Start the first strip's FP8 stream before anything else.
-  StripIn cur, nxt;
-  load_strip(J, row_base + wave * kStripRows, ecol, lane, cur);
-  const float tscale = J.scale_mode == 1 ? G(J.scales)[0] : 1.0f;
-
-  int koff[kMaxLoras];
+  LoraSteps LS;
   {
     int k0 = 0;
 #pragma unroll
     for (int l = 0; l < kMaxLoras; ++l) {
-      koff[l] = k0;
-      if (l < nl) k0 += pad_rank(J.lora[l].rank);
+      LS.kst[l] = k0;
+      LS.nks[l] = l < nl ? pad_rank(J.lora[l].rank) / 32 : 0;
+      k0 += LS.nks[l];
     }
+    LS.total = k0;
   }
-#pragma unroll
-  for (int l = 0; l < (MULTI ? kMaxLoras : 1); ++l) {
-    if (l >= nl) break;
-    stage_at(AT, ld, koff[l], J.lora[l], i0, cols, tid);
-  }
-  __syncthreads();
-
-  for (int s = 0; s < S; ++s) {
-    const int64_t r0 = row_base + (int64_t)(s * kWavesPerGroup + wave) * kStripRows;
-    if (r0 >= rows) break;
-    const int64_t r0n = r0 + kWavesPerGroup * kStripRows;
-    const bool more = s + 1 < S && r0n < rows;
-
-    f32x4 acc[2][8];
-    float cfin;
-    if (!MULTI) {
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
-      if (more) load_strip(J, r0n, ecol, lane, nxt);
-      lora_mfma(acc, AT, ld, koff[0], J.lora[0], r0, rows, ln, lg);
-      cfin = J.lora[0].coeff;
-    } else {
-      f32x4 delta[2][8];
-      if (more) load_strip(J, r0n, ecol, lane, nxt);
-#pragma unroll
-      for (int l = 0; l < kMaxLoras; ++l) {
-        if (l >= nl) break;
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-          for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
-        lora_mfma(acc, AT, ld, koff[l], J.lora[l], r0, rows, ln, lg);
-        const float c = J.lora[l].coeff;
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-          for (int nb = 0; nb < 8; ++nb)
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-              delta[mb][nb][v] = l == 0 ? c * acc[mb][nb][v] : __builtin_fmaf(c, acc[mb][nb][v], delta[mb][nb][v]);
-      }
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = delta[mb][nb];
-      cfin = 1.0f;
-    }
-
-    // --- Epilogue straight from registers.
-#pragma unroll
-    for (int g = 0; g < 8; ++g) {
-      const int mb = g >> 2, v = g & 3;
-      const int64_t r = r0 + 16 * mb + 4 * lg + v;
-      if (r < rows && ecol < cols) {
-        float x[8];
-        decode4(cur.w[g][0], J.fmt, x);
-        decode4(cur.w[g][1], J.fmt, x + 4);
-        const float sc = J.scale_mode == 2 ? cur.s[g] : tscale;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if (J.scale_mode != 0) x[j] = __builtin_fmaf(sc, x[j], 0.0f);
-          x[j] = canon_nan(__builtin_fmaf(cfin, acc[mb][j][v], x[j]));
-        }
-        if (F32OUT) {
-          auto dst = G(reinterpret_cast<f32x4*>(reinterpret_cast<float*>(J.out) + r * cols + ecol));
-          __builtin_nontemporal_store((f32x4){x[0], x[1], x[2], x[3]}, dst);
-          __builtin_nontemporal_store((f32x4){x[4], x[5], x[6], x[7]}, dst + 1);
-        } else {
-          const u32x4 o = {pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]), pack_bf16(x[4], x[5]), pack_bf16(x[6], x[7])};
-          __builtin_nontemporal_store(o, G(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(J.out) + r * cols + ecol)));
-        }
-      }
-    }
-    cur = nxt;
+  const bool full = (int64_t)g0 + kWavesPerGroup * kStripRows <= J.rows && (int64_t)i0 + kBandCols <= J.cols;
+  if (J.fmt == 0) {
+    if (full) fused_unit<F32OUT, MULTI, KS, true, 0>(J, LS, AT, tab.lds_ld, i0, g0, threadIdx.x);
+    else fused_unit<F32OUT, MULTI, KS, false, 0>(J, LS, AT, tab.lds_ld, i0, g0, threadIdx.x);
+  } else {
+    if (full) fused_unit<F32OUT, MULTI, KS, true, 1>(J, LS, AT, tab.lds_ld, i0, g0, threadIdx.x);
+    else fused_unit<F32OUT, MULTI, KS, false, 1>(J, LS, AT, tab.lds_ld, i0, g0, threadIdx.x);
   }
 }
 
@@ -416,18 +513,32 @@ hipError_t launch_dequant(const DequantArgs& a, int fmt, int scale_mode, bool f3
                   : dequant_dispatch_scale<1>(a, scale_mode, f32out, grid, stream);
 }
 
+template <int KS>
+hipError_t launch_fused_ks(const JobTable& t, bool f32out, bool multi, dim3 grid, size_t lds, hipStream_t stream) {
+  if (f32out) {
+    if (multi) hipLaunchKernelGGL((k_fused<true, true, KS>), grid, dim3(256), lds, stream, t);
+    else hipLaunchKernelGGL((k_fused<true, false, KS>), grid, dim3(256), lds, stream, t);
+  } else {
+    if (multi) hipLaunchKernelGGL((k_fused<false, true, KS>), grid, dim3(256), lds, stream, t);
+    else hipLaunchKernelGGL((k_fused<false, false, KS>), grid, dim3(256), lds, stream, t);
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, hipStream_t stream) {
   if (t.total_units == 0) return hipSuccess;
   dim3 grid((unsigned)t.total_units);
   size_t lds = (size_t)kBandCols * (size_t)t.lds_ld * sizeof(uint16_t);
-  if (f32out) {
-    if (multi) hipLaunchKernelGGL((k_fused<true, true>), grid, dim3(256), lds, stream, t);
-    else hipLaunchKernelGGL((k_fused<true, false>), grid, dim3(256), lds, stream, t);
-  } else {
-    if (multi) hipLaunchKernelGGL((k_fused<false, true>), grid, dim3(256), lds, stream, t);
-    else hipLaunchKernelGGL((k_fused<false, false>), grid, dim3(256), lds, stream, t);
+  switch ((t.lds_ld - 8) / 32) {  // K-steps of the largest job
+    case 1: return launch_fused_ks<1>(t, f32out, multi, grid, lds, stream);
+    case 2: return launch_fused_ks<2>(t, f32out, multi, grid, lds, stream);
+    case 3: return launch_fused_ks<3>(t, f32out, multi, grid, lds, stream);
+    case 4: return launch_fused_ks<4>(t, f32out, multi, grid, lds, stream);
+    case 5: return launch_fused_ks<5>(t, f32out, multi, grid, lds, stream);
+    case 6: return launch_fused_ks<6>(t, f32out, multi, grid, lds, stream);
+    case 7: return launch_fused_ks<7>(t, f32out, multi, grid, lds, stream);
+    default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 hipError_t launch_generic(const GenericArgs& a, bool f32out, hipStream_t stream) {
