@@ -1,19 +1,24 @@
 """Benchmark: fused FP8 dequant + LoRA merge on one MI355X.
 
-Workload (one step = one fused dequant + merge of one DiT linear layer):
+Default workload ("layer"; one step = one fused dequant + merge of one DiT
+linear layer):
   W 4096 (out) x 4096 (in) e4m3fn, per-output-row f32 scales U[1e-3, 1e-1],
   LoRA B 4096 x 64 and A 64 x 4096 bf16 ~ N(0, 0.02^2), alpha = 1, bf16 out.
-Inputs are resident in HBM before timing; consecutive steps rotate over
->= 1 GiB of distinct buffers so the 256 MB MALL cannot serve repeats.
+Other workloads (--workload): "dequant" (4096 x 4096 e4m3fn, one scale, no
+LoRA), "block" (one DiT block of 10 tensors in one grouped launch), "mixed"
+(e5m2 FFN / e4m3fn attention, two stacked LoRAs r32 + r128, 4104-wide edge
+tensors). Inputs are resident in HBM before timing; consecutive steps rotate
+over >= 1 GiB of distinct buffers so the 256 MB MALL cannot serve repeats.
 
 value     = algorithmic bytes per step * steps / timed seconds (GB/s), with
-            algorithmic bytes = out*in (FP8) + 2*out*in (bf16 out) + 4*out
-            (scales) + 2*r*(out+in) (bf16 factors).
+            algorithmic bytes = out*in (FP8) + 2*out*in (bf16 out) + scale
+            bytes + 2*r*(out+in) (bf16 factors) per tensor, timed with HIP
+            events on the library's compute stream.
 roofline  = that figure against MI355X's 8 TB/s HBM peak; `traffic` is the
-            rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch (scaled by the
-            same counters on a plain device copy) from profiles/, when present.
+            rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the
+            same counter on a plain device copy, from profiles/ when present.
 cpu_baseline = the CPU oracle (a C restatement of the reference's read path,
-            same operation order) on the same layer, on this host's cores.
+            same operation order) on the workload's first tensor, host cores.
 
 Prints exactly one JSON line on stdout; progress goes to stderr.
 """
@@ -33,7 +38,10 @@ METRIC = "dequant+LoRA-merge GB/s & % HBM roofline; s to materialise 22B weights
 HBM_PEAK_GBPS = 8000.0
 ROWS, COLS, RANK = 4096, 4096, 64
 ROTATE_BYTES = 1 << 30
-PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "fused_dequant_lora_4096x4096_r64.pmc.txt")
+PMC_SUMMARY = {
+    "layer": os.path.join(ROOT, "profiles", "k_fused_layer4096x4096_r64.pmc.txt"),
+    "block": os.path.join(ROOT, "profiles", "k_fused_ditblock_r64.pmc.txt"),
+}
 
 
 def log(*a):
@@ -74,12 +82,14 @@ class Hip:
         self._ok(self.L.hipMemcpyAsync(dst, src, n, 3, stream), "hipMemcpyAsync D2D")
 
 
-def read_traffic():
-    """Per-dispatch HBM bytes from the committed rocprofv3 PMC summary."""
-    if not os.path.exists(PROFILE_SUMMARY):
+def read_traffic(workload):
+    """Per-dispatch HBM bytes (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated
+    against a plain device copy) from the committed summary for `workload`."""
+    path = PMC_SUMMARY.get(workload)
+    if not path or not os.path.exists(path):
         return None
     vals = {}
-    with open(PROFILE_SUMMARY) as f:
+    with open(path) as f:
         for line in f:
             if ":" in line and line.strip().startswith("traffic_bytes_per_dispatch"):
                 try:
@@ -296,7 +306,7 @@ def main():
                    "params": int(sum(c["rows"] * c["cols"] for c in cases)), "rotating_instances": n_inst},
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBPS, 4),
-                     "traffic": read_traffic() if args.workload == "layer" else None,
+                     "traffic": read_traffic(args.workload),
                      "algorithmic_bytes": step_bytes, "lora_flops": flops,
                      "copy_ceiling_GBps": round(copy_gbps, 1), "frac_of_copy": round(value / copy_gbps, 4)},
         "cpu_baseline": cpu,

@@ -385,24 +385,60 @@ __device__ __forceinline__ void fused_unit(const JobDev& J, const LoraSteps& LS,
   for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  // Epilogue values of M-block mb, in place of its accumulators:
+  //   y = fma(scale, decode(w), coeff * (B A)), scale = 1 when unscaled.
+  // (The reference rounds scale*decode(w) first; one rounding fewer here.)
+  auto epi_values = [&](int mb, float c) {
+    if (c != 1.0f) {  // uniform; the coefficient is 1 in the common case
 #pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    if (t < LS.total) {
-      const int kk = 32 * t + 8 * lg;
+      for (int nb = 0; nb < 8; ++nb) acc[mb][nb] *= c;
+    }
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb) {
-        const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + kk]);
-        acc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[t][0], at, acc[0][nb], 0, 0, 0);
-        acc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[t][1], at, acc[1][nb], 0, 0, 0);
+    for (int v = 0; v < 4; ++v) {
+      const int g = 4 * mb + v;
+      float x[8];
+      decode4(wv[g][0], FMT, x);
+      decode4(wv[g][1], FMT, x + 4);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[mb][j][v] = __builtin_fmaf(sc[g], x[j], acc[mb][j][v]);
+    }
+  };
+
+  if (!MULTI) {
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      if (t < LS.total) {
+        const int kk = 32 * t + 8 * lg;
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+          const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + kk]);
+          acc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[t][0], at, acc[0][nb], 0, 0, 0);
+          acc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[t][1], at, acc[1][nb], 0, 0, 0);
+        }
       }
-      if (MULTI) {
+    }
+    const float c = J.lora[0].coeff;
+    epi_values(0, c);
+    epi_values(1, c);
+  } else {
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      if (t < LS.total) {
+        const int kk = 32 * t + 8 * lg;
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+          const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + kk]);
+          acc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[t][0], at, acc[0][nb], 0, 0, 0);
+          acc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[t][1], at, acc[1][nb], 0, 0, 0);
+        }
         // Last K-step of its LoRA: fold coeff * (B A) into the running sum.
         const StepInfo si = step_info(LS, t);
         if (si.last) {
-          float c = J.lora[0].coeff;
+          float cl = J.lora[0].coeff;
 #pragma unroll
           for (int q = 1; q < kMaxLoras; ++q)
-            if (si.l == q) c = J.lora[q].coeff;
+            if (si.l == q) cl = J.lora[q].coeff;
           const bool first = si.l == 0;
 #pragma unroll
           for (int mb = 0; mb < 2; ++mb)
@@ -410,36 +446,47 @@ __device__ __forceinline__ void fused_unit(const JobDev& J, const LoraSteps& LS,
             for (int nb = 0; nb < 8; ++nb) {
 #pragma unroll
               for (int v = 0; v < 4; ++v)
-                delta[mb][nb][v] = first ? c * acc[mb][nb][v] : __builtin_fmaf(c, acc[mb][nb][v], delta[mb][nb][v]);
+                delta[mb][nb][v] = first ? cl * acc[mb][nb][v] : __builtin_fmaf(cl, acc[mb][nb][v], delta[mb][nb][v]);
               acc[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
             }
         }
       }
     }
-  }
-  float cfin = J.lora[0].coeff;
-  if (MULTI) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = delta[mb][nb];
-    cfin = 1.0f;
+    epi_values(0, 1.0f);
+    epi_values(1, 1.0f);
   }
 
-  // 4. Epilogue straight from registers:
-  //    out = RNE(fma(cfin, delta, fma(scale, decode(w), 0))), scale = 1 when unscaled.
+  // 4. Canonical NaNs (one wave-wide test), RNE to bf16, stores.
+  {
+    uint64_t any = 0;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) any |= __builtin_amdgcn_ballot_w64(__builtin_isnan(acc[mb][nb][v]));
+    if (any) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[mb][nb][v] = canon_nan(acc[mb][nb][v]);
+    }
+  }
 #pragma unroll
   for (int g = 0; g < 8; ++g) {
     const int mb = g >> 2, v = g & 3;
     const uint32_t dr = 16 * mb + v;
     if (col_ok && (FULL || rl + dr < rows)) {
-      float x[8];
-      decode4(wv[g][0], FMT, x);
-      decode4(wv[g][1], FMT, x + 4);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = __builtin_fmaf(cfin, acc[mb][j][v], __builtin_fmaf(sc[g], x[j], 0.0f));
-      canon_nan_wave<8>(x);
       const uint32_t e = e0 + dr * cols;
+      float x[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = acc[mb][j][v];
       if (F32OUT) {
         st_nt_at<f32x4>(J.out, 4 * e, (f32x4){x[0], x[1], x[2], x[3]});
         st_nt_at<f32x4>(J.out, 4 * e + 16, (f32x4){x[4], x[5], x[6], x[7]});
