@@ -41,8 +41,17 @@ typedef enum {
   LTXW_ERR_NO_LORA_MATCHES = 11 /* WeightError::NoLoraMatches */
 } ltxw_status;
 
-/* FP8 storage formats (safetensors "F8_E4M3" / "F8_E5M2"; src/fp8.rs:3-7). */
-typedef enum { LTXW_FMT_E4M3FN = 0, LTXW_FMT_E5M2 = 1 } ltxw_fp8_format;
+/* Base-weight storage formats: the FP8 formats of the hot path (safetensors
+ * "F8_E4M3" / "F8_E5M2"; src/fp8.rs:3-7) and the other dtypes `read` widens
+ * (src/store.rs:672-729: "BF16", "F16", "F32"). Scales apply to FP8 only
+ * (src/store.rs:500); the non-FP8 formats take the one-element-per-thread path. */
+typedef enum {
+  LTXW_FMT_E4M3FN = 0,
+  LTXW_FMT_E5M2 = 1,
+  LTXW_FMT_BF16 = 2,
+  LTXW_FMT_F16 = 3,
+  LTXW_FMT_F32 = 4
+} ltxw_format;
 
 /* Scale convention. TENSOR is the reference's `{key}_scale` scalar
  * (src/store.rs:498-508: v = fma(scale, v, 0)). ROW (one f32 per output row,
@@ -56,25 +65,39 @@ typedef enum { LTXW_OUT_BF16 = 0, LTXW_OUT_F32 = 1 } ltxw_out_dtype;
 /* Maximum LoRAs merged into one tensor in a single launch. */
 #define LTXW_MAX_LORAS 4
 
+/* Element type of LoRA factors (src/lora.rs:176-209 widens all of them to
+ * f32 exactly). BF16 (zero, the default) takes the MFMA path; the others take
+ * the one-element-per-thread path in the reference's operation order. */
+typedef enum {
+  LTXW_FACTOR_BF16 = 0,
+  LTXW_FACTOR_F32 = 1,
+  LTXW_FACTOR_F16 = 2,
+  LTXW_FACTOR_E4M3FN = 3,
+  LTXW_FACTOR_E5M2 = 4
+} ltxw_factor_dtype;
+
 /* One low-rank delta coeff * (B @ A), the device form of the reference's
- * `LowRankDelta` (src/store.rs:751-763). B is bf16 [rows x rank] row-major
- * (`prefix.lora_B.weight`), A is bf16 [rank x cols] row-major
- * (`prefix.lora_A.weight`), coeff = strength * alpha / rank (src/store.rs:615). */
+ * `LowRankDelta` (src/store.rs:751-763). B is [rows x rank] row-major
+ * (`prefix.lora_B.weight`), A is [rank x cols] row-major
+ * (`prefix.lora_A.weight`), both of element type `dtype`, aligned to it;
+ * coeff = strength * alpha / rank (src/store.rs:615). */
 typedef struct {
-  const uint16_t* b;
-  const uint16_t* a;
+  const void* b;
+  const void* a;
   int32_t rank;
   float coeff;
+  int32_t dtype;     /* ltxw_factor_dtype */
+  int32_t reserved;  /* 0 */
 } ltxw_lora;
 
 /* One tensor to materialise in a grouped launch. */
 typedef struct {
-  const uint8_t* w;        /* device FP8 [rows x cols] */
+  const uint8_t* w;        /* device [rows x cols] in `fmt` (element-aligned) */
   void* out;               /* device bf16 or f32 [rows x cols] */
   const float* scales;     /* device f32: 1 (TENSOR) or rows (ROW) values; NULL for NONE */
   int64_t rows;
   int64_t cols;
-  int32_t fmt;             /* ltxw_fp8_format */
+  int32_t fmt;             /* ltxw_format */
   int32_t scale_mode;      /* ltxw_scale_mode */
   int32_t out_dtype;       /* ltxw_out_dtype */
   int32_t n_loras;         /* 0..LTXW_MAX_LORAS, merged in array order */
@@ -85,9 +108,14 @@ typedef struct ltxw_ctx ltxw_ctx;
 
 /* Create a context on HIP device `device` with a ring of `n_staging` pinned
  * host buffers of `staging_bytes` each for host->device uploads (0 picks
- * 64 MiB x 4). No reference counterpart: the reference has no device. */
+ * 32 MiB x 16; allocated on first use). No reference counterpart: the
+ * reference has no device. */
 int ltxw_ctx_create(int device, size_t staging_bytes, int n_staging, ltxw_ctx** out);
 void ltxw_ctx_destroy(ltxw_ctx* ctx);
+
+/* Host threads that copy mapped file bytes into the pinned ring during
+ * ltxw_store_materialize (default min(8, hardware threads)). */
+int ltxw_ctx_set_host_threads(ltxw_ctx* ctx, int n);
 
 /* Message of the last failed call on this context ("" if none). With a NULL
  * context, the message of the last failed ltxw_ctx_create on this thread. */
@@ -110,8 +138,9 @@ int ltxw_download(ltxw_ctx* ctx, const void* src, size_t bytes, void* host_dst);
 /* Wait until all work queued on the context has finished. */
 int ltxw_synchronize(ltxw_ctx* ctx);
 
-/* FP8 -> out_dtype dequantisation of one [rows x cols] tensor:
- * out = RNE(fma(scale, LUT[w], 0)) (or RNE(LUT[w]) for NONE).
+/* Dequantisation of one [rows x cols] tensor to out_dtype:
+ * out = RNE(fma(scale, LUT[w], 0)) (or RNE(LUT[w]) for NONE); non-FP8
+ * formats are widened exactly and take no scale.
  * Replaces the decode + scale of `WeightStore::read` (src/store.rs:488-508). */
 int ltxw_dequant(ltxw_ctx* ctx, const uint8_t* w, int64_t rows, int64_t cols, int fmt,
                  int scale_mode, const float* scales, void* out, int out_dtype);

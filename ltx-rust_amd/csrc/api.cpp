@@ -11,42 +11,23 @@
 #include <string.h>
 
 #include <algorithm>
+#include <map>
 #include <mutex>
+#include <thread>
+#include <tuple>
 #include <new>
 #include <string>
 #include <vector>
 
+#include "ctx.h"
 #include "kernels.h"
 #include "ltxw.h"
 
-struct ltxw_ctx {
-  int device = 0;
-  int cu_count = 256;
-  hipStream_t compute = nullptr;
-  hipStream_t copy = nullptr;
-  // Pinned staging ring for host -> device uploads.
-  std::vector<void*> stage;
-  std::vector<hipEvent_t> stage_done;
-  size_t stage_bytes = 0;
-  size_t next_stage = 0;
-  // Job tables of grouped launches: a ring of pinned host mirrors -> device
-  // buffers, so that the host can queue several launches ahead of the GPU.
-  struct TableSlot {
-    void* host = nullptr;
-    void* dev = nullptr;
-    size_t cap = 0;
-    hipEvent_t copied = nullptr;  // recorded after the slot's last upload
-  };
-  std::vector<TableSlot> tables;
-  size_t next_table = 0;
-  std::string err;
-};
-
 namespace {
-
 thread_local std::string g_create_err;
+}  // namespace
 
-int fail(ltxw_ctx* ctx, int code, const char* fmt, ...) {
+int ltxw::fail(ltxw_ctx* ctx, int code, const char* fmt, ...) {
   char buf[512];
   va_list ap;
   va_start(ap, fmt);
@@ -55,6 +36,10 @@ int fail(ltxw_ctx* ctx, int code, const char* fmt, ...) {
   if (ctx) ctx->err = buf; else g_create_err = buf;
   return code;
 }
+
+namespace {
+
+using ltxw::fail;
 
 int hip_fail(ltxw_ctx* ctx, hipError_t e, const char* what) {
   return fail(ctx, LTXW_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
@@ -67,6 +52,18 @@ int hip_fail(ltxw_ctx* ctx, hipError_t e, const char* what) {
   } while (0)
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Bytes per LoRA factor element (ltxw_factor_dtype); 0 for an unknown type.
+int factor_bytes(int dt) {
+  switch (dt) {
+    case LTXW_FACTOR_BF16:
+    case LTXW_FACTOR_F16: return 2;
+    case LTXW_FACTOR_F32: return 4;
+    case LTXW_FACTOR_E4M3FN:
+    case LTXW_FACTOR_E5M2: return 1;
+    default: return 0;
+  }
+}
 
 // rows * cols without overflow; false when either is negative or it overflows.
 bool elem_count(int64_t rows, int64_t cols, uint64_t* n) {
@@ -100,16 +97,21 @@ int check_extent(ltxw_ctx* ctx, const void* p, uint64_t bytes, const char* what)
 int check_desc(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t* n) {
   if (!elem_count(d.rows, d.cols, n))
     return fail(ctx, LTXW_ERR_INVALID_ARG, "invalid shape [%lld, %lld]", (long long)d.rows, (long long)d.cols);
-  if (d.fmt != LTXW_FMT_E4M3FN && d.fmt != LTXW_FMT_E5M2)
-    return fail(ctx, LTXW_ERR_UNSUPPORTED, "unsupported FP8 format %d", d.fmt);
+  const int esize = ltxw::format_bytes(d.fmt);
+  if (esize == 0) return fail(ctx, LTXW_ERR_UNSUPPORTED, "unsupported weight format %d", d.fmt);
   if (d.scale_mode < LTXW_SCALE_NONE || d.scale_mode > LTXW_SCALE_ROW)
     return fail(ctx, LTXW_ERR_INVALID_ARG, "invalid scale mode %d", d.scale_mode);
+  // store.rs:500: the `{key}_scale` sibling applies to FP8 tensors only.
+  if (esize != 1 && d.scale_mode != LTXW_SCALE_NONE)
+    return fail(ctx, LTXW_ERR_INVALID_ARG, "scales apply to FP8 formats only (format %d)", d.fmt);
   if (d.out_dtype != LTXW_OUT_BF16 && d.out_dtype != LTXW_OUT_F32)
     return fail(ctx, LTXW_ERR_INVALID_ARG, "invalid output dtype %d", d.out_dtype);
   if (d.n_loras < 0 || d.n_loras > LTXW_MAX_LORAS)
     return fail(ctx, LTXW_ERR_INVALID_ARG, "n_loras %d outside [0, %d]", d.n_loras, LTXW_MAX_LORAS);
   if (*n == 0) return LTXW_OK;
   if (!d.w || !d.out) return fail(ctx, LTXW_ERR_INVALID_ARG, "null weight or output pointer");
+  if (!aligned(d.w, (size_t)esize))
+    return fail(ctx, LTXW_ERR_INVALID_ARG, "weight pointer is not aligned to its %d-byte elements", esize);
   if (d.scale_mode != LTXW_SCALE_NONE && !d.scales)
     return fail(ctx, LTXW_ERR_INVALID_ARG, "scale mode %d needs a scales pointer", d.scale_mode);
   for (int l = 0; l < d.n_loras; ++l) {
@@ -119,17 +121,22 @@ int check_desc(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t* n) {
       return fail(ctx, LTXW_ERR_LORA_RANK, "LoRA %d has rank %d", l, L.rank);
     if (L.rank > (1 << 20)) return fail(ctx, LTXW_ERR_INVALID_ARG, "LoRA %d rank %d is too large", l, L.rank);
     if (!L.a || !L.b) return fail(ctx, LTXW_ERR_INVALID_ARG, "LoRA %d has a null factor", l);
+    const int fs = factor_bytes(L.dtype);
+    if (fs == 0) return fail(ctx, LTXW_ERR_UNSUPPORTED, "LoRA %d has unsupported factor type %d", l, L.dtype);
+    if (!aligned(L.a, (size_t)fs) || !aligned(L.b, (size_t)fs))
+      return fail(ctx, LTXW_ERR_INVALID_ARG, "LoRA %d factors are not aligned to their %d-byte elements", l, fs);
   }
   int rc;
-  if ((rc = check_extent(ctx, d.w, *n, "weight"))) return rc;
+  if ((rc = check_extent(ctx, d.w, *n * (uint64_t)esize, "weight"))) return rc;
   if ((rc = check_extent(ctx, d.out, *n * (d.out_dtype == LTXW_OUT_F32 ? 4 : 2), "output"))) return rc;
   if (d.scale_mode != LTXW_SCALE_NONE &&
       (rc = check_extent(ctx, d.scales, 4 * (d.scale_mode == LTXW_SCALE_ROW ? (uint64_t)d.rows : 1), "scales")))
     return rc;
   for (int l = 0; l < d.n_loras; ++l) {
     const ltxw_lora& L = d.loras[l];
-    if ((rc = check_extent(ctx, L.b, 2 * (uint64_t)d.rows * (uint64_t)L.rank, "LoRA B"))) return rc;
-    if ((rc = check_extent(ctx, L.a, 2 * (uint64_t)L.rank * (uint64_t)d.cols, "LoRA A"))) return rc;
+    const uint64_t fs = (uint64_t)factor_bytes(L.dtype);
+    if ((rc = check_extent(ctx, L.b, fs * (uint64_t)d.rows * (uint64_t)L.rank, "LoRA B"))) return rc;
+    if ((rc = check_extent(ctx, L.a, fs * (uint64_t)L.rank * (uint64_t)d.cols, "LoRA A"))) return rc;
   }
   return LTXW_OK;
 }
@@ -144,13 +151,16 @@ ltxw::JobDev to_job(const ltxw_tensor_desc& d) {
   j.fmt = d.fmt;
   j.scale_mode = d.scale_mode;
   j.n_loras = d.n_loras;
-  for (int l = 0; l < d.n_loras; ++l) j.lora[l] = {d.loras[l].b, d.loras[l].a, d.loras[l].rank, d.loras[l].coeff};
+  for (int l = 0; l < d.n_loras; ++l)
+    j.lora[l] = {(const uint16_t*)d.loras[l].b, (const uint16_t*)d.loras[l].a, d.loras[l].rank, d.loras[l].coeff,
+                 d.loras[l].dtype, 0};
   j.bands_n = (int32_t)((d.cols + ltxw::kBandCols - 1) / ltxw::kBandCols);
   return j;
 }
 
 // The tiled MFMA kernel's layout requirements (else: generic kernel).
 bool fused_ok(const ltxw_tensor_desc& d) {
+  if (ltxw::format_bytes(d.fmt) != 1) return false;
   if (d.cols % 8 != 0 || !aligned(d.w, 16) || !aligned(d.out, 16)) return false;
   if (d.scale_mode == LTXW_SCALE_ROW && !aligned(d.scales, 16)) return false;  // read 4 rows at a time
   // The kernel addresses every buffer with 32-bit byte offsets.
@@ -159,6 +169,7 @@ bool fused_ok(const ltxw_tensor_desc& d) {
   int k = 0;
   for (int l = 0; l < d.n_loras; ++l) {
     const uint64_t r = (uint64_t)d.loras[l].rank;
+    if (d.loras[l].dtype != LTXW_FACTOR_BF16) return false;
     if (r % 8 != 0 || !aligned(d.loras[l].a, 16) || !aligned(d.loras[l].b, 16)) return false;
     if (2 * r * (uint64_t)d.rows > lim || 2 * r * (uint64_t)d.cols > lim) return false;
     k += ltxw::pad_rank(d.loras[l].rank);
@@ -257,38 +268,69 @@ int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool 
   return LTXW_OK;
 }
 
-int run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n) {
+}  // namespace
+
+int ltxw::run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n) {
   // Validate everything before queuing anything.
   std::vector<uint64_t> counts((size_t)n);
   for (int k = 0; k < n; ++k) {
     int rc = check_desc(ctx, descs[k], &counts[(size_t)k]);
     if (rc) return rc;
   }
-  // Four fused buckets: (f32 out, multi-LoRA).
-  std::vector<ltxw::JobDev> bucket[2][2];
+  // Fused launches are bucketed by (f32 out, multi-LoRA, K-steps), so that the
+  // register arrays of each launch are sized for its own jobs' rank, not for
+  // the largest rank of the call.
+  std::map<std::tuple<int, int, int>, std::vector<ltxw::JobDev>> buckets;
   for (int k = 0; k < n; ++k) {
     const ltxw_tensor_desc& d = descs[k];
     uint64_t cnt = counts[(size_t)k];
     if (cnt == 0) continue;
     int rc = LTXW_OK;
-    if (d.n_loras == 0) {
+    if (d.n_loras == 0 && ltxw::format_bytes(d.fmt) == 1) {
       rc = run_dequant(ctx, d, cnt);
     } else if (fused_ok(d)) {
-      bucket[d.out_dtype == LTXW_OUT_F32][d.n_loras > 1].push_back(to_job(d));
+      ltxw::JobDev j = to_job(d);
+      buckets[{d.out_dtype == LTXW_OUT_F32, d.n_loras > 1, job_k(j) / 32}].push_back(j);
     } else {
       rc = run_generic(ctx, d, 0, cnt);
     }
     if (rc) return rc;
   }
-  for (int f = 0; f < 2; ++f)
-    for (int m = 0; m < 2; ++m) {
-      int rc = run_fused(ctx, bucket[f][m], f == 1, m == 1);
-      if (rc) return rc;
-    }
+  for (auto& kv : buckets) {
+    int rc = run_fused(ctx, kv.second, std::get<0>(kv.first) == 1, std::get<1>(kv.first) == 1);
+    if (rc) return rc;
+  }
   return LTXW_OK;
 }
 
-}  // namespace
+int ltxw::ensure_staging(ltxw_ctx* ctx) {
+  if (!ctx->stage.empty()) return LTXW_OK;
+  for (int k = 0; k < ctx->n_stage; ++k) {
+    void* p = nullptr;
+    hipEvent_t ev = nullptr;
+    if (hipHostMalloc(&p, ctx->stage_bytes, hipHostMallocDefault) != hipSuccess) {
+      (void)hipGetLastError();
+      for (void* q : ctx->stage) (void)hipHostFree(q);
+      for (hipEvent_t e : ctx->stage_done) (void)hipEventDestroy(e);
+      ctx->stage.clear();
+      ctx->stage_done.clear();
+      return fail(ctx, LTXW_ERR_OOM, "pinned staging buffer of %zu bytes", ctx->stage_bytes);
+    }
+    ctx->stage.push_back(p);
+    hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      ctx->stage_done.push_back(nullptr);
+      for (void* q : ctx->stage) (void)hipHostFree(q);
+      for (hipEvent_t x : ctx->stage_done) if (x) (void)hipEventDestroy(x);
+      ctx->stage.clear();
+      ctx->stage_done.clear();
+      return hip_fail(ctx, e, "staging event");
+    }
+    ctx->stage_done.push_back(ev);
+  }
+  ctx->next_stage = 0;
+  return LTXW_OK;
+}
 
 extern "C" {
 
@@ -300,12 +342,14 @@ int ltxw_ctx_create(int device, size_t staging_bytes, int n_staging, ltxw_ctx** 
   if (e != hipSuccess) return fail(nullptr, LTXW_ERR_HIP, "hipGetDeviceCount: %s", hipGetErrorString(e));
   if (device < 0 || device >= ndev)
     return fail(nullptr, LTXW_ERR_INVALID_ARG, "device %d not in [0, %d)", device, ndev);
-  if (staging_bytes == 0) staging_bytes = 64u << 20;
-  if (n_staging <= 0) n_staging = 4;
+  if (staging_bytes == 0) staging_bytes = 32u << 20;
+  if (n_staging <= 0) n_staging = 16;
   ltxw_ctx* c = new (std::nothrow) ltxw_ctx();
   if (!c) return fail(nullptr, LTXW_ERR_OOM, "context allocation");
   c->device = device;
   c->stage_bytes = staging_bytes;
+  c->n_stage = n_staging;
+  c->host_threads = (int)std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
   auto bail = [&](int code, const char* what, hipError_t he) {
     g_create_err = std::string(what) + ": " + hipGetErrorString(he);
     ltxw_ctx_destroy(c);
@@ -322,16 +366,6 @@ int ltxw_ctx_create(int device, size_t staging_bytes, int n_staging, ltxw_ctx** 
   for (auto& t : c->tables)
     if ((e = hipEventCreateWithFlags(&t.copied, hipEventDisableTiming)) != hipSuccess)
       return bail(LTXW_ERR_HIP, "event", e);
-  for (int k = 0; k < n_staging; ++k) {
-    void* p = nullptr;
-    hipEvent_t ev = nullptr;
-    if ((e = hipHostMalloc(&p, staging_bytes, hipHostMallocDefault)) != hipSuccess)
-      return bail(LTXW_ERR_OOM, "pinned staging buffer", e);
-    c->stage.push_back(p);
-    if ((e = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess)
-      return bail(LTXW_ERR_HIP, "event", e);
-    c->stage_done.push_back(ev);
-  }
   *out = c;
   return LTXW_OK;
 }
@@ -343,6 +377,9 @@ void ltxw_ctx_destroy(ltxw_ctx* ctx) {
   if (ctx->copy) (void)hipStreamSynchronize(ctx->copy);
   for (void* p : ctx->stage) (void)hipHostFree(p);
   for (hipEvent_t ev : ctx->stage_done) (void)hipEventDestroy(ev);
+  for (void* p : ctx->ring) (void)hipFree(p);
+  for (hipEvent_t ev : ctx->ring_free) (void)hipEventDestroy(ev);
+  for (hipEvent_t ev : ctx->ring_ready) (void)hipEventDestroy(ev);
   for (auto& t : ctx->tables) {
     if (t.host) (void)hipHostFree(t.host);
     if (t.dev) (void)hipFree(t.dev);
@@ -358,6 +395,13 @@ const char* ltxw_last_error(const ltxw_ctx* ctx) {
 }
 
 void* ltxw_ctx_stream(ltxw_ctx* ctx) { return ctx ? (void*)ctx->compute : nullptr; }
+
+int ltxw_ctx_set_host_threads(ltxw_ctx* ctx, int n) {
+  if (!ctx) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context");
+  if (n < 1 || n > 256) return fail(ctx, LTXW_ERR_INVALID_ARG, "host thread count %d outside [1, 256]", n);
+  ctx->host_threads = n;
+  return LTXW_OK;
+}
 
 int ltxw_alloc(ltxw_ctx* ctx, size_t bytes, void** dptr) {
   if (!ctx || !dptr) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context or output pointer");
@@ -393,6 +437,7 @@ int ltxw_upload(ltxw_ctx* ctx, const void* host_src, size_t bytes, void* dst) {
   if (!ctx) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context");
   if (bytes == 0) return LTXW_OK;
   if (!host_src || !dst) return fail(ctx, LTXW_ERR_INVALID_ARG, "null source or destination");
+  if (int rc = ltxw::ensure_staging(ctx)) return rc;
   const char* src = (const char*)host_src;
   size_t done = 0;
   while (done < bytes) {
@@ -452,13 +497,13 @@ int ltxw_dequant_lora(ltxw_ctx* ctx, const uint8_t* w, int64_t rows, int64_t col
   d.out_dtype = out_dtype;
   d.n_loras = n_loras;
   for (int l = 0; l < n_loras; ++l) d.loras[l] = loras[l];
-  return run_descs(ctx, &d, 1);
+  return ltxw::run_descs(ctx, &d, 1);
 }
 
 int ltxw_dequant_lora_grouped(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n) {
   if (!ctx) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context");
   if (n < 0 || (n > 0 && !descs)) return fail(ctx, LTXW_ERR_INVALID_ARG, "invalid descriptor array");
-  return run_descs(ctx, descs, n);
+  return ltxw::run_descs(ctx, descs, n);
 }
 
 }  // extern "C"

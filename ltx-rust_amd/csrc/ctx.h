@@ -1,0 +1,70 @@
+// The context object behind the C ABI and the internal calls shared by the
+// kernel entry points (api.cpp) and the weight store (store.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+#include <vector>
+
+#include "ltxw.h"
+
+struct ltxw_ctx {
+  int device = 0;
+  int cu_count = 256;
+  int host_threads = 8;
+  hipStream_t compute = nullptr;
+  hipStream_t copy = nullptr;
+  // Pinned staging ring for host -> device uploads (allocated on first use).
+  // Slot k may be refilled once stage_done[k] (recorded on the copy stream
+  // after the slot's last copy) has completed.
+  std::vector<void*> stage;
+  std::vector<hipEvent_t> stage_done;
+  size_t stage_bytes = 0;
+  int n_stage = 0;
+  size_t next_stage = 0;
+  // Job tables of grouped launches: a ring of pinned host mirrors -> device
+  // buffers, so that the host can queue several launches ahead of the GPU.
+  struct TableSlot {
+    void* host = nullptr;
+    void* dev = nullptr;
+    size_t cap = 0;
+    hipEvent_t copied = nullptr;  // recorded after the slot's last upload
+  };
+  std::vector<TableSlot> tables;
+  size_t next_table = 0;
+  // Device ring of the store's materialisation pipeline: FP8 bytes, scales
+  // and factors of one batch of tensors per slot. `ring_free[k]` is recorded
+  // on the compute stream after the last kernel that read slot k;
+  // `ring_ready[k]` on the copy stream after the slot's last copy.
+  std::vector<void*> ring;
+  std::vector<hipEvent_t> ring_free, ring_ready;
+  size_t ring_bytes = 0;
+  std::string err;
+};
+
+namespace ltxw {
+
+// Records a formatted message on ctx (or the thread's create error) and returns code.
+int fail(ltxw_ctx* ctx, int code, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
+
+// Allocates the pinned staging ring if it is not there yet.
+int ensure_staging(ltxw_ctx* ctx);
+
+// Validates and queues the descriptors on the compute stream (the body of
+// ltxw_dequant_lora_grouped).
+int run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n);
+
+// Bytes per element of a base format (ltxw_format); 0 for an unknown one.
+inline int format_bytes(int fmt) {
+  switch (fmt) {
+    case LTXW_FMT_E4M3FN:
+    case LTXW_FMT_E5M2: return 1;
+    case LTXW_FMT_BF16:
+    case LTXW_FMT_F16: return 2;
+    case LTXW_FMT_F32: return 4;
+    default: return 0;
+  }
+}
+
+}  // namespace ltxw

@@ -19,10 +19,12 @@ constexpr int kWavesPerGroup = 4;
 constexpr int kRankMax = 224;  // 128 slots x (224 + 8) bf16 = 59 KB of LDS
 
 struct LoraDev {
-  const uint16_t* b;  // bf16 [rows x rank]
-  const uint16_t* a;  // bf16 [rank x cols]
+  const uint16_t* b;  // [rows x rank], element type `dtype` (bf16 on the fused path)
+  const uint16_t* a;  // [rank x cols]
   int32_t rank;
   float coeff;
+  int32_t dtype;      // 0 bf16, 1 f32, 2 f16, 3 e4m3fn, 4 e5m2
+  int32_t pad;
 };
 
 // One tensor of a fused launch, as the kernel reads it.

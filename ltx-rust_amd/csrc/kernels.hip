@@ -72,6 +72,45 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __builtin_bit_cast(float, (uint32_t)h << 16);
 }
 
+// IEEE binary16 -> f32, exact; a NaN keeps sign and payload and gets the
+// quiet bit (as `half`'s f16::to_f32, store.rs:690-705).
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  if ((h & 0x7C00u) == 0x7C00u && (h & 0x3FFu))
+    return __builtin_bit_cast(float, ((uint32_t)(h & 0x8000u) << 16) | 0x7FC00000u | ((uint32_t)(h & 0x3FFu) << 13));
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// f32 -> bf16, round to nearest even; a NaN keeps sign and the top payload
+// bits and gets the quiet bit (half's bf16::from_f32).
+__device__ __forceinline__ uint16_t bf16_rne(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  return (uint16_t)(pack_bf16(v, 0.0f) & 0xFFFFu);
+}
+
+// Element e of a LoRA factor of element type dt (0 bf16, 1 f32, 2 f16,
+// 3 e4m3fn, 4 e5m2), widened exactly as lora.rs:176-209 does.
+__device__ __forceinline__ float load_factor(const void* p, int dt, uint64_t e) {
+  switch (dt) {
+    case 0: return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[e]);
+    case 1: return reinterpret_cast<const float*>(p)[e];
+    case 2: return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[e]);
+    default: return canon_nan(decode1(reinterpret_cast<const uint8_t*>(p)[e], dt - 3));
+  }
+}
+
+// Element e of a base tensor in any of the accepted formats
+// (0 e4m3fn, 1 e5m2, 2 bf16, 3 f16, 4 f32; store.rs:672-729).
+__device__ __forceinline__ float load_base(const JobDev& J, uint64_t e) {
+  switch (J.fmt) {
+    case 0:
+    case 1: return canon_nan(decode1(J.w[e], J.fmt));
+    case 2: return bf16_to_f32(reinterpret_cast<const uint16_t*>(J.w)[e]);
+    case 3: return f16_to_f32(reinterpret_cast<const uint16_t*>(J.w)[e]);
+    default: return reinterpret_cast<const float*>(J.w)[e];
+  }
+}
+
 // Pointers read out of job descriptors are generic; marking them global makes
 // the compiler emit global_load/global_store (not flat_*, which also count
 // against the LDS counter and skip the global addressing modes).
@@ -160,24 +199,26 @@ __global__ __launch_bounds__(256) void k_generic(GenericArgs g) {
   uint64_t e = g.elem_begin + k;
   uint64_t cols = (uint64_t)J.cols;
   uint64_t o = e / cols, i = e % cols;
-  float v = decode1(J.w[e], J.fmt);
+  float v = load_base(J, e);
   if (J.scale_mode == 1) v = __builtin_fmaf(J.scales[0], v, 0.0f);
   if (J.scale_mode == 2) v = __builtin_fmaf(J.scales[o], v, 0.0f);
 #pragma unroll
   for (int l = 0; l < kMaxLoras; ++l) {
     if (l >= J.n_loras) break;
     const LoraDev L = J.lora[l];
-    const uint16_t* brow = L.b + o * (uint64_t)L.rank;
+    const uint64_t brow = o * (uint64_t)L.rank;
     for (int r = 0; r < L.rank; ++r) {
-      float c = L.coeff * bf16_to_f32(brow[r]);
-      v = __builtin_fmaf(c, bf16_to_f32(L.a[(uint64_t)r * cols + i]), v);
+      float c = L.coeff * load_factor(L.b, L.dtype, brow + r);
+      v = __builtin_fmaf(c, load_factor(L.a, L.dtype, (uint64_t)r * cols + i), v);
     }
   }
-  v = canon_nan(v);
+  // FP8 sources: a NaN can only come from a NaN code (decoded canonical) or
+  // the arithmetic, and the reference's is canonical too.
+  if (J.fmt <= 1) v = canon_nan(v);
   if (F32OUT)
     reinterpret_cast<float*>(J.out)[e] = v;
   else
-    reinterpret_cast<uint16_t*>(J.out)[e] = (uint16_t)(pack_bf16(v, 0.0f) & 0xFFFFu);
+    reinterpret_cast<uint16_t*>(J.out)[e] = bf16_rne(v);
 }
 
 // ---------------------------------------------------------------------------

@@ -1,0 +1,972 @@
+// Weight store (include/ltxw_store.h): memory-mapped safetensors files, key
+// renaming, LoRA files and merge bookkeeping, and the staged
+// host -> HBM materialisation pipeline that feeds the dequant / LoRA kernels.
+//
+// Reference: crates/ltx-weights/src/store.rs (WeightStore), src/lora.rs
+// (LoraFile, MergeReport), src/key_map.rs (KeyMap::apply_key).
+#include <fcntl.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <condition_variable>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+#include "ctx.h"
+#include "ltxw_store.h"
+#include "safetensors.h"
+
+namespace st = ltxw::st;
+
+namespace {
+
+thread_local std::string g_err;
+
+int sfail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int sfail(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+// ---------------------------------------------------------------------------
+// Mapped files.
+// ---------------------------------------------------------------------------
+struct MappedFile {
+  std::string path;
+  int fd = -1;
+  const uint8_t* base = nullptr;
+  uint64_t size = 0;
+  ~MappedFile() {
+    if (base) munmap(const_cast<uint8_t*>(base), size);
+    if (fd >= 0) close(fd);
+  }
+};
+
+// Opens and maps `path` read-only; the mapping lives as long as any holder
+// (store.rs:131-133 keeps its Mmaps for the store's lifetime).
+int map_file(const char* path, std::shared_ptr<MappedFile>* out) {
+  auto f = std::make_shared<MappedFile>();
+  f->path = path;
+  f->fd = open(path, O_RDONLY | O_CLOEXEC);
+  if (f->fd < 0) return sfail(LTXW_ERR_IO, "%s: %s", path, strerror(errno));
+  struct stat sb;
+  if (fstat(f->fd, &sb) != 0) return sfail(LTXW_ERR_IO, "%s: %s", path, strerror(errno));
+  f->size = (uint64_t)sb.st_size;
+  if (f->size > 0) {
+    void* p = mmap(nullptr, f->size, PROT_READ, MAP_SHARED, f->fd, 0);
+    if (p == MAP_FAILED) return sfail(LTXW_ERR_IO, "%s: mmap: %s", path, strerror(errno));
+    f->base = (const uint8_t*)p;
+  }
+  *out = std::move(f);
+  return LTXW_OK;
+}
+
+int parse_file(const MappedFile& f, st::Header* h) {
+  std::string msg;
+  if (st::parse(f.base, f.size, h, &msg) != st::OK)
+    return sfail(LTXW_ERR_FORMAT, "%s: safetensors: %s", f.path.c_str(), msg.c_str());
+  return LTXW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Exact host widening of small tensors (scales, alpha, LoRA factors read on
+// the host), per element type: src/store.rs:672-729, src/lora.rs:176-209.
+// ---------------------------------------------------------------------------
+float f_bits(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+float with_sign(uint32_t sign, float mag) {
+  uint32_t u;
+  memcpy(&u, &mag, 4);
+  return f_bits(sign | u);
+}
+
+float e4m3fn_f32(uint8_t b) {  // src/fp8.rs:90-120
+  if ((b & 0x7F) == 0x7F) return f_bits(0x7FC00000u);  // f32::NAN for both signs
+  uint32_t sign = (uint32_t)(b & 0x80) << 24, e = (b >> 3) & 0xF, m = b & 7;
+  if (e == 0) return with_sign(sign, std::ldexp((float)m, -9));  // exact
+  return f_bits(sign | (e + 120) << 23 | m << 20);
+}
+
+float e5m2_f32(uint8_t b) {  // src/fp8.rs:127-158
+  uint32_t sign = (uint32_t)(b & 0x80) << 24, e = (b >> 2) & 0x1F, m = b & 3;
+  if (e == 31) return m ? f_bits(0x7FC00000u) : f_bits(sign | 0x7F800000u);
+  if (e == 0) return with_sign(sign, std::ldexp((float)m, -16));
+  return f_bits(sign | (e + 112) << 23 | m << 21);
+}
+
+float f16_f32(uint16_t h) {  // half's f16::to_f32: exact; NaN quiet, payload kept
+  uint32_t sign = (uint32_t)(h & 0x8000) << 16, e = (h >> 10) & 0x1F, m = h & 0x3FF;
+  if (e == 31) return f_bits(sign | (m ? 0x7FC00000u | m << 13 : 0x7F800000u));
+  if (e == 0) return with_sign(sign, std::ldexp((float)m, -24));
+  return f_bits(sign | (e + 112) << 23 | m << 13);
+}
+
+bool decodable(int32_t dt) {
+  return dt == st::F32 || dt == st::F16 || dt == st::BF16 || dt == st::F8_E4M3 || dt == st::F8_E5M2;
+}
+
+// Little-endian, unaligned-safe.
+void decode_host(const uint8_t* p, int32_t dt, uint64_t n, float* out) {
+  for (uint64_t k = 0; k < n; ++k) {
+    switch (dt) {
+      case st::F8_E4M3: out[k] = e4m3fn_f32(p[k]); break;
+      case st::F8_E5M2: out[k] = e5m2_f32(p[k]); break;
+      case st::BF16: out[k] = f_bits((uint32_t)(p[2 * k] | p[2 * k + 1] << 8) << 16); break;
+      case st::F16: out[k] = f16_f32((uint16_t)(p[2 * k] | p[2 * k + 1] << 8)); break;
+      default: {
+        uint32_t u;
+        memcpy(&u, p + 4 * k, 4);
+        out[k] = f_bits(u);
+      }
+    }
+  }
+}
+
+// Base formats the device path takes (ltxw_format), or -1.
+int device_format(int32_t dt) {
+  switch (dt) {
+    case st::F8_E4M3: return LTXW_FMT_E4M3FN;
+    case st::F8_E5M2: return LTXW_FMT_E5M2;
+    case st::BF16: return LTXW_FMT_BF16;
+    case st::F16: return LTXW_FMT_F16;
+    case st::F32: return LTXW_FMT_F32;
+    default: return -1;
+  }
+}
+
+// LoRA factor element types the device path takes (ltxw_factor_dtype); the
+// store only merges decodable ones.
+int factor_dtype(int32_t dt) {
+  switch (dt) {
+    case st::F32: return LTXW_FACTOR_F32;
+    case st::F16: return LTXW_FACTOR_F16;
+    case st::F8_E4M3: return LTXW_FACTOR_E4M3FN;
+    case st::F8_E5M2: return LTXW_FACTOR_E5M2;
+    default: return LTXW_FACTOR_BF16;
+  }
+}
+
+uint64_t factor_size(int fdt) {
+  return fdt == LTXW_FACTOR_F32 ? 4 : (fdt == LTXW_FACTOR_E4M3FN || fdt == LTXW_FACTOR_E5M2) ? 1 : 2;
+}
+
+uint64_t dim_or(const std::vector<uint64_t>& s, size_t i, uint64_t dflt) { return i < s.size() ? s[i] : dflt; }
+
+// `usize_to_f32` (src/store.rs:745-750).
+float rank_f32(uint64_t r) { return r > UINT32_MAX ? 3.40282347e38f : (float)(uint32_t)r; }
+
+bool ends_with(const std::string& s, const std::string& t) {
+  return s.size() >= t.size() && s.compare(s.size() - t.size(), t.size(), t) == 0;
+}
+bool starts_with(const std::string& s, const std::string& t) { return s.compare(0, t.size(), t) == 0; }
+
+// ---------------------------------------------------------------------------
+// Key rules (`KeyMap::apply_key`, src/key_map.rs:237-268).
+// ---------------------------------------------------------------------------
+struct Rule {
+  int32_t kind;
+  std::vector<std::string> s;
+};
+
+bool apply_key(const std::vector<Rule>& rules, std::string* key) {
+  for (const Rule& r : rules) {
+    switch (r.kind) {
+      case LTXW_RULE_REQUIRE_ANY_PREFIX: {
+        if (r.s.empty()) break;
+        bool any = false;
+        for (const auto& p : r.s) any = any || starts_with(*key, p);
+        if (!any) return false;
+        break;
+      }
+      case LTXW_RULE_REPLACE: {
+        const std::string& f = r.s[0];
+        if (f.empty() || key->find(f) == std::string::npos) {
+          // An empty pattern matches before every character and at the end
+          // (Rust's str::replace), so the replacement is inserted there.
+          if (f.empty()) {
+            std::string out = r.s[1];
+            size_t i = 0;
+            while (i < key->size()) {
+              // step over one UTF-8 character
+              size_t len = 1;
+              unsigned char c = (unsigned char)(*key)[i];
+              if (c >= 0xF0) len = 4; else if (c >= 0xE0) len = 3; else if (c >= 0xC0) len = 2;
+              out.append(*key, i, len);
+              out += r.s[1];
+              i += len;
+            }
+            *key = out;
+          }
+          break;
+        }
+        std::string out;
+        size_t pos = 0, hit;
+        while ((hit = key->find(f, pos)) != std::string::npos) {
+          out.append(*key, pos, hit - pos);
+          out += r.s[1];
+          pos = hit + f.size();
+        }
+        out.append(*key, pos, std::string::npos);
+        *key = out;
+        break;
+      }
+      case LTXW_RULE_RENAME_EXACT:
+        if (starts_with(*key, r.s[0])) *key = r.s[1] + key->substr(r.s[0].size());
+        break;
+      case LTXW_RULE_DROP_PREFIX:
+        if (starts_with(*key, r.s[0])) return false;
+        break;
+      case LTXW_RULE_DROP_SUFFIX:
+        if (ends_with(*key, r.s[0])) return false;
+        break;
+      default: break;
+    }
+  }
+  return true;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Objects behind the opaque handles.
+// ---------------------------------------------------------------------------
+struct LoraData {
+  std::shared_ptr<MappedFile> file;
+  std::unordered_map<std::string, st::TensorInfo> tensors;  // offsets absolute in the file
+  std::vector<std::string> names;                           // sorted
+  std::map<std::string, std::string> metadata;
+};
+
+struct ltxw_lora_file {
+  std::shared_ptr<LoraData> d;
+};
+
+struct ltxw_merge_report {
+  std::vector<std::string> matched, unmatched;
+};
+
+namespace {
+
+struct Entry {
+  int32_t dtype;
+  std::vector<uint64_t> shape;
+  uint32_t file;
+  uint64_t start, end;  // absolute in the file
+  uint64_t numel;
+};
+
+// One merged low-rank delta (src/store.rs:751-763), kept as the adapter's
+// own bytes: the LoRA file stays mapped while the store holds the delta.
+struct Delta {
+  std::shared_ptr<LoraData> lora;
+  std::string key_a, key_b;
+  uint64_t rank, out, in;
+  float coeff;
+};
+
+}  // namespace
+
+struct ltxw_store {
+  std::vector<std::shared_ptr<MappedFile>> files;
+  std::unordered_map<std::string, Entry> entries;
+  std::unordered_set<std::string> scale_keys;
+  std::map<std::string, std::string> metadata;
+  std::unordered_map<std::string, std::vector<Delta>> deltas;
+  std::vector<std::string> visible;  // sorted
+};
+
+namespace {
+
+int tensor_info_out(int32_t dtype, const std::vector<uint64_t>& shape, int32_t* dt, int32_t* ndim,
+                    int64_t* dims, int32_t max_dims) {
+  if (dt) *dt = dtype;
+  if (ndim) *ndim = (int32_t)shape.size();
+  if (dims)
+    for (int32_t k = 0; k < max_dims && k < (int32_t)shape.size(); ++k) dims[k] = (int64_t)shape[(size_t)k];
+  return LTXW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Materialisation plan of one key.
+// ---------------------------------------------------------------------------
+constexpr uint64_t kAlign = 256;
+uint64_t align_up(uint64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+struct Plan {
+  const std::string* key;
+  const Entry* e;
+  const uint8_t* wsrc;  // mapped weight bytes
+  void* out;
+  int fmt, esize;
+  uint64_t rows, cols, numel;
+  int scale_mode;
+  std::vector<float> scales;
+  std::vector<const Delta*> deltas;
+  const uint8_t* fb[LTXW_MAX_LORAS];  // mapped factor bytes
+  const uint8_t* fa[LTXW_MAX_LORAS];
+  int fdt[LTXW_MAX_LORAS];            // ltxw_factor_dtype
+  // Offsets inside the batch's device slot.
+  uint64_t off_w, off_s, off_b[LTXW_MAX_LORAS], off_a[LTXW_MAX_LORAS], bytes;
+};
+
+int make_plan(const ltxw_store* s, const std::string& key, uint32_t flags, int out_dtype, void* out, Plan* p) {
+  auto it = s->entries.find(key);
+  if (it == s->entries.end()) return sfail(LTXW_ERR_MISSING_KEY, "missing key: \"%s\"", key.c_str());
+  const Entry& e = it->second;
+  p->key = &it->first;
+  p->e = &e;
+  p->wsrc = s->files[e.file]->base + e.start;
+  p->out = out;
+  p->fmt = device_format(e.dtype);
+  if (p->fmt < 0)
+    return sfail(LTXW_ERR_UNSUPPORTED, "unsupported dtype %s for key \"%s\"", st::dtype_name(e.dtype), key.c_str());
+  p->esize = ltxw::format_bytes(p->fmt);
+  p->numel = e.numel;
+  p->rows = e.shape.empty() ? 1 : e.shape[0];
+  p->cols = p->rows ? p->numel / p->rows : 0;
+  if (p->numel && !out) return sfail(LTXW_ERR_INVALID_ARG, "null output buffer for key \"%s\"", key.c_str());
+  (void)out_dtype;
+
+  // FP8 scale sibling (store.rs:498-508).
+  p->scale_mode = LTXW_SCALE_NONE;
+  if (st::is_fp8(e.dtype)) {
+    auto sc = s->entries.find(key + "_scale");
+    if (sc != s->entries.end()) {
+      const Entry& se = sc->second;
+      if (!decodable(se.dtype))
+        return sfail(LTXW_ERR_UNSUPPORTED, "unsupported dtype %s for key \"%s_scale\"", st::dtype_name(se.dtype),
+                     key.c_str());
+      const uint8_t* base = s->files[se.file]->base + se.start;
+      const bool rows = !(flags & LTXW_MAT_SCALE_FIRST) && e.shape.size() >= 2 && e.shape[0] > 1 &&
+                        se.numel == e.shape[0];
+      if (rows) {
+        p->scales.resize(se.numel);
+        decode_host(base, se.dtype, se.numel, p->scales.data());
+        p->scale_mode = LTXW_SCALE_ROW;
+      } else {
+        // decode_scalar_f32 (store.rs:732-735): element 0, or 1.0 when empty.
+        float v = 1.0f;
+        if (se.numel) decode_host(base, se.dtype, 1, &v);
+        p->scales.assign(1, v);
+        p->scale_mode = LTXW_SCALE_TENSOR;
+      }
+    }
+  }
+
+  // Merged deltas (store.rs:510-515, add_to's checks at :767-779).
+  auto dl = s->deltas.find(key);
+  if (dl != s->deltas.end()) {
+    if (dl->second.size() > (size_t)LTXW_MAX_LORAS)
+      return sfail(LTXW_ERR_UNSUPPORTED, "key \"%s\" has %zu merged LoRAs; the device path takes at most %d",
+                   key.c_str(), dl->second.size(), LTXW_MAX_LORAS);
+    for (const Delta& d : dl->second) {
+      const uint64_t out_in = d.out * d.in;
+      if ((d.in && out_in / d.in != d.out) || out_in != p->numel || d.in == 0 || d.rank == 0)
+        return sfail(LTXW_ERR_LORA_SHAPE, "LoRA shape mismatch for key \"%s\"", key.c_str());
+      const st::TensorInfo& ta = d.lora->tensors.at(d.key_a);
+      const st::TensorInfo& tb = d.lora->tensors.at(d.key_b);
+      if (ta.dtype != tb.dtype)
+        return sfail(LTXW_ERR_UNSUPPORTED, "LoRA factors of \"%s\" mix %s (B) and %s (A)", key.c_str(),
+                     st::dtype_name(tb.dtype), st::dtype_name(ta.dtype));
+      if (d.rank > (1u << 20))
+        return sfail(LTXW_ERR_UNSUPPORTED, "LoRA rank %llu of \"%s\" is too large", (unsigned long long)d.rank,
+                     key.c_str());
+      const size_t l = p->deltas.size();
+      p->fb[l] = d.lora->file->base + tb.begin;
+      p->fa[l] = d.lora->file->base + ta.begin;
+      p->fdt[l] = factor_dtype(ta.dtype);
+      p->deltas.push_back(&d);
+    }
+    if (!p->deltas.empty()) {
+      p->rows = p->deltas[0]->out;
+      p->cols = p->deltas[0]->in;
+    }
+  }
+
+  // Device layout of the payload: weight, scales, then (B, A) per delta.
+  uint64_t off = 0;
+  p->off_w = off;
+  off = align_up(off + p->numel * (uint64_t)p->esize);
+  p->off_s = off;
+  off = align_up(off + 4 * (uint64_t)p->scales.size());
+  for (size_t l = 0; l < p->deltas.size(); ++l) {
+    const Delta& d = *p->deltas[l];
+    const uint64_t fs = factor_size(p->fdt[l]);
+    p->off_b[l] = off;
+    off = align_up(off + fs * d.out * d.rank);
+    p->off_a[l] = off;
+    off = align_up(off + fs * d.rank * d.in);
+  }
+  p->bytes = off;
+  return LTXW_OK;
+}
+
+
+// One host->device copy of the pipeline: at most one staging buffer.
+struct Piece {
+  const uint8_t* src;
+  uint64_t len;
+  uint64_t dst;  // offset in the batch's device slot
+};
+
+struct Batch {
+  size_t first_plan, n_plans;
+  size_t first_piece, end_piece;
+};
+
+// Creates the three-slot device ring (or grows it to `need` bytes per slot).
+int ensure_ring(ltxw_ctx* ctx, uint64_t need) {
+  hipError_t he;
+  if (ctx->ring_free.empty()) {
+    for (int k = 0; k < 3; ++k) {
+      hipEvent_t a = nullptr, b = nullptr;
+      if ((he = hipEventCreateWithFlags(&a, hipEventDisableTiming)) != hipSuccess)
+        return sfail(LTXW_ERR_HIP, "ring event: %s", hipGetErrorString(he));
+      ctx->ring_free.push_back(a);
+      if ((he = hipEventCreateWithFlags(&b, hipEventDisableTiming)) != hipSuccess)
+        return sfail(LTXW_ERR_HIP, "ring event: %s", hipGetErrorString(he));
+      ctx->ring_ready.push_back(b);
+    }
+  }
+  if (!ctx->ring.empty() && ctx->ring_bytes >= need) return LTXW_OK;
+  if (!ctx->ring.empty()) {
+    if ((he = hipStreamSynchronize(ctx->copy)) != hipSuccess || (he = hipStreamSynchronize(ctx->compute)) != hipSuccess)
+      return sfail(LTXW_ERR_HIP, "device ring resize: %s", hipGetErrorString(he));
+    for (void* q : ctx->ring) (void)hipFree(q);
+    ctx->ring.clear();
+    ctx->ring_bytes = 0;
+  }
+  for (int k = 0; k < 3; ++k) {
+    void* q = nullptr;
+    if (hipMalloc(&q, need) != hipSuccess) {
+      (void)hipGetLastError();
+      for (void* x : ctx->ring) (void)hipFree(x);
+      ctx->ring.clear();
+      return sfail(LTXW_ERR_OOM, "device staging ring of 3 x %llu bytes", (unsigned long long)need);
+    }
+    ctx->ring.push_back(q);
+  }
+  ctx->ring_bytes = need;
+  for (int k = 0; k < 3; ++k)  // nothing reads the fresh slots
+    if ((he = hipEventRecord(ctx->ring_free[(size_t)k], ctx->compute)) != hipSuccess)
+      return sfail(LTXW_ERR_HIP, "ring event record: %s", hipGetErrorString(he));
+  return LTXW_OK;
+}
+
+// Staged pipeline over `plans` (each with numel > 0):
+//   host threads: mapped bytes -> pinned staging slot (slot p % S for piece p,
+//                 refilled once the copy of piece p - S has completed);
+//   this thread:  pinned slot -> device ring slot on the copy stream, in
+//                 piece order; after a batch's last piece, the compute stream
+//                 waits for the copies and runs the batch's kernels.
+// Host reads finish before return; device work completes in stream order.
+int run_pipeline(ltxw_ctx* ctx, std::vector<Plan>& plans, int out_dtype) {
+  if (plans.empty()) return LTXW_OK;
+  hipError_t he;
+  if ((he = hipSetDevice(ctx->device)) != hipSuccess)
+    return sfail(LTXW_ERR_HIP, "hipSetDevice: %s", hipGetErrorString(he));
+  if (int rc = ltxw::ensure_staging(ctx)) return sfail(rc, "%s", ctx->err.c_str());
+  uint64_t need = 512ull << 20;
+  for (const Plan& p : plans) need = std::max(need, p.bytes);
+  if (int rc = ensure_ring(ctx, need)) return rc;
+  const uint64_t stage = ctx->stage_bytes;
+  const size_t S = ctx->stage.size(), R = ctx->ring.size();
+
+  std::vector<Batch> batches;
+  std::vector<Piece> pieces;
+  auto add = [&](const void* src, uint64_t len, uint64_t dst) {
+    for (uint64_t o = 0; o < len; o += stage)
+      pieces.push_back({(const uint8_t*)src + o, std::min(stage, len - o), dst + o});
+  };
+  for (size_t k = 0; k < plans.size();) {
+    Batch b{k, 0, pieces.size(), 0};
+    uint64_t used = 0;
+    while (k < plans.size() && (b.n_plans == 0 || used + plans[k].bytes <= ctx->ring_bytes)) {
+      Plan& p = plans[k];
+      p.off_w += used;
+      p.off_s += used;
+      for (size_t l = 0; l < p.deltas.size(); ++l) {
+        p.off_b[l] += used;
+        p.off_a[l] += used;
+      }
+      add(p.wsrc, p.numel * (uint64_t)p.esize, p.off_w);
+      if (!p.scales.empty()) add(p.scales.data(), 4 * p.scales.size(), p.off_s);
+      for (size_t l = 0; l < p.deltas.size(); ++l) {
+        const Delta& d = *p.deltas[l];
+        const uint64_t fs = factor_size(p.fdt[l]);
+        add(p.fb[l], fs * d.out * d.rank, p.off_b[l]);
+        add(p.fa[l], fs * d.rank * d.in, p.off_a[l]);
+      }
+      used += p.bytes;
+      ++b.n_plans;
+      ++k;
+    }
+    b.end_piece = pieces.size();
+    batches.push_back(b);
+  }
+
+  // Shared state of the host copy threads.
+  std::mutex mu;
+  std::condition_variable cv;
+  std::vector<uint8_t> filled(pieces.size(), 0);
+  size_t recorded = 0;  // pieces whose copy-done event has been recorded
+  bool abort = false;
+  std::string worker_err;
+  std::atomic<size_t> next{0};
+  const int device = ctx->device;
+
+  auto worker = [&]() {
+    (void)hipSetDevice(device);
+    for (;;) {
+      const size_t p = next.fetch_add(1);
+      if (p >= pieces.size()) return;
+      const size_t s = p % S;
+      {
+        std::unique_lock<std::mutex> lk(mu);
+        cv.wait(lk, [&] { return abort || p < recorded + S; });
+        if (abort) return;
+      }
+      // The slot's previous copy (piece p - S, or an earlier call's) is done.
+      hipError_t e = hipEventSynchronize(ctx->stage_done[s]);
+      if (e != hipSuccess) {
+        std::lock_guard<std::mutex> lk(mu);
+        abort = true;
+        worker_err = std::string("staging wait: ") + hipGetErrorString(e);
+        cv.notify_all();
+        return;
+      }
+      memcpy(ctx->stage[s], pieces[p].src, pieces[p].len);
+      {
+        std::lock_guard<std::mutex> lk(mu);
+        filled[p] = 1;
+      }
+      cv.notify_all();
+    }
+  };
+  const int nt = std::max(1, std::min<int>(ctx->host_threads, (int)pieces.size()));
+  std::vector<std::thread> threads;
+  threads.reserve((size_t)nt);
+  for (int t = 0; t < nt; ++t) threads.emplace_back(worker);
+
+  int rc = LTXW_OK;
+  std::vector<ltxw_tensor_desc> descs;
+  for (size_t bi = 0; bi < batches.size() && rc == LTXW_OK; ++bi) {
+    const Batch& b = batches[bi];
+    const size_t slot = bi % R;
+    char* base = (char*)ctx->ring[slot];
+    // Copies into the slot wait for the kernels that last read it.
+    if ((he = hipStreamWaitEvent(ctx->copy, ctx->ring_free[slot], 0)) != hipSuccess) {
+      rc = sfail(LTXW_ERR_HIP, "copy stream wait: %s", hipGetErrorString(he));
+      break;
+    }
+    for (size_t p = b.first_piece; p < b.end_piece; ++p) {
+      {
+        std::unique_lock<std::mutex> lk(mu);
+        cv.wait(lk, [&] { return abort || filled[p]; });
+        if (abort) {
+          rc = sfail(LTXW_ERR_HIP, "%s", worker_err.c_str());
+          break;
+        }
+      }
+      const size_t s = p % S;
+      if ((he = hipMemcpyAsync(base + pieces[p].dst, ctx->stage[s], pieces[p].len, hipMemcpyHostToDevice,
+                               ctx->copy)) != hipSuccess ||
+          (he = hipEventRecord(ctx->stage_done[s], ctx->copy)) != hipSuccess) {
+        rc = sfail(LTXW_ERR_HIP, "staged copy: %s", hipGetErrorString(he));
+        break;
+      }
+      {
+        std::lock_guard<std::mutex> lk(mu);
+        recorded = p + 1;
+      }
+      cv.notify_all();
+    }
+    if (rc) break;
+    if ((he = hipEventRecord(ctx->ring_ready[slot], ctx->copy)) != hipSuccess ||
+        (he = hipStreamWaitEvent(ctx->compute, ctx->ring_ready[slot], 0)) != hipSuccess) {
+      rc = sfail(LTXW_ERR_HIP, "batch hand-off: %s", hipGetErrorString(he));
+      break;
+    }
+    descs.clear();
+    for (size_t k = b.first_plan; k < b.first_plan + b.n_plans; ++k) {
+      const Plan& p = plans[k];
+      ltxw_tensor_desc d{};
+      d.w = (const uint8_t*)(base + p.off_w);
+      d.out = p.out;
+      d.scales = p.scales.empty() ? nullptr : (const float*)(base + p.off_s);
+      d.rows = (int64_t)p.rows;
+      d.cols = (int64_t)p.cols;
+      d.fmt = p.fmt;
+      d.scale_mode = p.scale_mode;
+      d.out_dtype = out_dtype;
+      d.n_loras = (int32_t)p.deltas.size();
+      for (size_t l = 0; l < p.deltas.size(); ++l)
+        d.loras[l] = {base + p.off_b[l], base + p.off_a[l], (int32_t)p.deltas[l]->rank, p.deltas[l]->coeff,
+                      p.fdt[l], 0};
+      descs.push_back(d);
+    }
+    if (int r2 = ltxw::run_descs(ctx, descs.data(), (int)descs.size())) {
+      rc = sfail(r2, "%s", ctx->err.c_str());
+      break;
+    }
+    if ((he = hipEventRecord(ctx->ring_free[slot], ctx->compute)) != hipSuccess) {
+      rc = sfail(LTXW_ERR_HIP, "ring event record: %s", hipGetErrorString(he));
+      break;
+    }
+  }
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    if (rc) abort = true;
+  }
+  cv.notify_all();
+  for (auto& t : threads) t.join();
+  return rc;
+}
+
+int materialize(ltxw_store* s, ltxw_ctx* ctx, const char* const* keys, int64_t n_keys, int32_t out_dtype,
+                uint32_t flags, void* const* outs) {
+  if (!s || !ctx) return sfail(LTXW_ERR_INVALID_ARG, "null store or context");
+  if (n_keys < 0 || (n_keys > 0 && (!keys || !outs)))
+    return sfail(LTXW_ERR_INVALID_ARG, "invalid key or output array");
+  if (out_dtype != LTXW_OUT_BF16 && out_dtype != LTXW_OUT_F32)
+    return sfail(LTXW_ERR_INVALID_ARG, "invalid output dtype %d", out_dtype);
+  if (flags & ~LTXW_MAT_SCALE_FIRST) return sfail(LTXW_ERR_INVALID_ARG, "unknown flags 0x%x", flags);
+  // Resolve and check every key before any work is queued.
+  std::vector<Plan> plans;
+  plans.reserve((size_t)n_keys);
+  for (int64_t k = 0; k < n_keys; ++k) {
+    if (!keys[k]) return sfail(LTXW_ERR_INVALID_ARG, "null key at index %lld", (long long)k);
+    Plan p{};
+    if (int rc = make_plan(s, keys[k], flags, out_dtype, outs[k], &p)) return rc;
+    if (p.numel) plans.push_back(std::move(p));
+  }
+  return run_pipeline(ctx, plans, out_dtype);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI.
+// ---------------------------------------------------------------------------
+extern "C" {
+
+const char* ltxw_store_last_error(void) { return g_err.c_str(); }
+
+int ltxw_store_open(const char* const* paths, int n_paths, const ltxw_key_rule* rules, int n_rules,
+                    ltxw_store** out) {
+  if (!out) return sfail(LTXW_ERR_INVALID_ARG, "null output pointer");
+  *out = nullptr;
+  if (n_paths < 0 || (n_paths > 0 && !paths) || n_rules < 0 || (n_rules > 0 && !rules))
+    return sfail(LTXW_ERR_INVALID_ARG, "invalid path or rule array");
+  std::vector<Rule> rs;
+  for (int k = 0; k < n_rules; ++k) {
+    const ltxw_key_rule& r = rules[k];
+    int want = -1;
+    switch (r.kind) {
+      case LTXW_RULE_REQUIRE_ANY_PREFIX: want = -2; break;
+      case LTXW_RULE_REPLACE:
+      case LTXW_RULE_RENAME_EXACT: want = 2; break;
+      case LTXW_RULE_DROP_PREFIX:
+      case LTXW_RULE_DROP_SUFFIX: want = 1; break;
+      case LTXW_RULE_SPLIT_QKV:
+      case LTXW_RULE_FOLD_GATES:
+      case LTXW_RULE_SYNTH_ZERO_TYPE_EMB:
+        return sfail(LTXW_ERR_UNSUPPORTED, "key rule %d (open-time value transform) is not supported", r.kind);
+      default: return sfail(LTXW_ERR_INVALID_ARG, "unknown key rule kind %d", r.kind);
+    }
+    if (r.n < 0 || (want >= 0 && r.n != want) || (r.n > 0 && !r.strs))
+      return sfail(LTXW_ERR_INVALID_ARG, "key rule %d: kind %d takes %d strings, got %d", k, r.kind, want, r.n);
+    Rule x{r.kind, {}};
+    for (int j = 0; j < r.n; ++j) {
+      if (!r.strs[j]) return sfail(LTXW_ERR_INVALID_ARG, "key rule %d: null string", k);
+      x.s.emplace_back(r.strs[j]);
+    }
+    rs.push_back(std::move(x));
+  }
+  std::unique_ptr<ltxw_store> s(new (std::nothrow) ltxw_store());
+  if (!s) return sfail(LTXW_ERR_OOM, "store allocation");
+  for (int fi = 0; fi < n_paths; ++fi) {
+    if (!paths[fi]) return sfail(LTXW_ERR_INVALID_ARG, "null path at index %d", fi);
+    std::shared_ptr<MappedFile> f;
+    if (int rc = map_file(paths[fi], &f)) return rc;
+    st::Header h;
+    if (int rc = parse_file(*f, &h)) return rc;
+    for (const auto& kv : h.metadata) s->metadata.emplace(kv.first, kv.second);  // first file wins
+    for (const auto& t : h.tensors) {
+      std::string name = t.first;
+      if (!apply_key(rs, &name)) continue;
+      if (s->entries.count(name)) return sfail(LTXW_ERR_DUPLICATE_KEY, "duplicate key \"%s\" across checkpoint files",
+                                               name.c_str());
+      Entry e{t.second.dtype, t.second.shape, (uint32_t)s->files.size(), h.data_start + t.second.begin,
+              h.data_start + t.second.end, t.second.numel()};
+      s->entries.emplace(std::move(name), std::move(e));
+    }
+    s->files.push_back(std::move(f));
+  }
+  // `{key}_scale` of an FP8 `key` is internal (store.rs:174-187).
+  for (const auto& kv : s->entries) {
+    const std::string& k = kv.first;
+    if (!ends_with(k, "_scale")) continue;
+    auto it = s->entries.find(k.substr(0, k.size() - 6));
+    if (it != s->entries.end() && st::is_fp8(it->second.dtype)) s->scale_keys.insert(k);
+  }
+  for (const auto& kv : s->entries)
+    if (!s->scale_keys.count(kv.first)) s->visible.push_back(kv.first);
+  std::sort(s->visible.begin(), s->visible.end());
+  *out = s.release();
+  return LTXW_OK;
+}
+
+void ltxw_store_close(ltxw_store* s) { delete s; }
+
+int64_t ltxw_store_n_keys(const ltxw_store* s) { return s ? (int64_t)s->visible.size() : 0; }
+
+const char* ltxw_store_key(const ltxw_store* s, int64_t index) {
+  if (!s || index < 0 || index >= (int64_t)s->visible.size()) return nullptr;
+  return s->visible[(size_t)index].c_str();
+}
+
+int ltxw_store_contains(const ltxw_store* s, const char* key) {
+  if (!s || !key) return 0;
+  return s->entries.count(key) && !s->scale_keys.count(key) ? 1 : 0;
+}
+
+int ltxw_store_tensor_info(const ltxw_store* s, const char* key, int32_t* dtype, int32_t* ndim, int64_t* shape,
+                           int32_t max_dims) {
+  if (!s || !key) return sfail(LTXW_ERR_INVALID_ARG, "null store or key");
+  auto it = s->entries.find(key);
+  if (it == s->entries.end()) return sfail(LTXW_ERR_MISSING_KEY, "missing key: \"%s\"", key);
+  return tensor_info_out(it->second.dtype, it->second.shape, dtype, ndim, shape, max_dims);
+}
+
+const char* ltxw_store_metadata(const ltxw_store* s, const char* key) {
+  if (!s || !key) return nullptr;
+  auto it = s->metadata.find(key);
+  return it == s->metadata.end() ? nullptr : it->second.c_str();
+}
+
+int ltxw_lora_open(const char* path, ltxw_lora_file** out) {
+  if (!out || !path) return sfail(LTXW_ERR_INVALID_ARG, "null path or output pointer");
+  *out = nullptr;
+  auto d = std::make_shared<LoraData>();
+  if (int rc = map_file(path, &d->file)) return rc;
+  st::Header h;
+  if (int rc = parse_file(*d->file, &h)) return rc;
+  d->metadata = h.metadata;
+  for (auto& t : h.tensors) {
+    st::TensorInfo ti = t.second;
+    ti.begin += h.data_start;
+    ti.end += h.data_start;
+    d->names.push_back(t.first);
+    d->tensors.emplace(t.first, ti);
+  }
+  std::sort(d->names.begin(), d->names.end());
+  ltxw_lora_file* f = new (std::nothrow) ltxw_lora_file();
+  if (!f) return sfail(LTXW_ERR_OOM, "LoRA file allocation");
+  f->d = std::move(d);
+  *out = f;
+  return LTXW_OK;
+}
+
+void ltxw_lora_close(ltxw_lora_file* f) { delete f; }
+
+int64_t ltxw_lora_n_tensors(const ltxw_lora_file* f) { return f ? (int64_t)f->d->names.size() : 0; }
+
+const char* ltxw_lora_tensor_name(const ltxw_lora_file* f, int64_t index) {
+  if (!f || index < 0 || index >= (int64_t)f->d->names.size()) return nullptr;
+  return f->d->names[(size_t)index].c_str();
+}
+
+int ltxw_lora_tensor_info(const ltxw_lora_file* f, const char* name, int32_t* dtype, int32_t* ndim, int64_t* shape,
+                          int32_t max_dims) {
+  if (!f || !name) return sfail(LTXW_ERR_INVALID_ARG, "null LoRA file or name");
+  auto it = f->d->tensors.find(name);
+  if (it == f->d->tensors.end()) return sfail(LTXW_ERR_MISSING_KEY, "missing key: \"%s\"", name);
+  return tensor_info_out(it->second.dtype, it->second.shape, dtype, ndim, shape, max_dims);
+}
+
+const char* ltxw_lora_metadata(const ltxw_lora_file* f, const char* key) {
+  if (!f || !key) return nullptr;
+  auto it = f->d->metadata.find(key);
+  return it == f->d->metadata.end() ? nullptr : it->second.c_str();
+}
+
+int ltxw_lora_ic_layout(const ltxw_lora_file* f, uint32_t* downscale, uint32_t* temporal) {
+  if (!f || !downscale || !temporal) return sfail(LTXW_ERR_INVALID_ARG, "null argument");
+  // parse_u32_meta (lora.rs:211-213): trimmed, an optional '+', decimal digits.
+  auto parse = [&](const char* key) -> uint32_t {
+    auto it = f->d->metadata.find(key);
+    if (it == f->d->metadata.end()) return 1;
+    const std::string& v = it->second;
+    size_t a = 0, b = v.size();
+    while (a < b && isspace((unsigned char)v[a])) ++a;
+    while (b > a && isspace((unsigned char)v[b - 1])) --b;
+    if (a < b && v[a] == '+') ++a;
+    if (a == b) return 1;
+    uint64_t x = 0;
+    for (size_t i = a; i < b; ++i) {
+      if (v[i] < '0' || v[i] > '9') return 1;
+      x = x * 10 + (uint64_t)(v[i] - '0');
+      if (x > UINT32_MAX) return 1;
+    }
+    return (uint32_t)x;
+  };
+  uint32_t d = parse("reference_downscale_factor"), t = parse("reference_temporal_scale_factor");
+  // IcLoraLayout::new (ltx-shape src/lib.rs:228-242) rejects a zero factor.
+  if (d == 0) return sfail(LTXW_ERR_INVALID_ARG, "shape error: reference scale factor %u", d);
+  if (t == 0) return sfail(LTXW_ERR_INVALID_ARG, "shape error: reference scale factor %u", t);
+  *downscale = d;
+  *temporal = t;
+  return LTXW_OK;
+}
+
+int ltxw_lora_read_f32(const ltxw_lora_file* f, const char* name, float* out, int64_t n) {
+  if (!f || !name) return sfail(LTXW_ERR_INVALID_ARG, "null LoRA file or name");
+  auto it = f->d->tensors.find(name);
+  if (it == f->d->tensors.end()) return sfail(LTXW_ERR_MISSING_KEY, "missing key: \"%s\"", name);
+  const st::TensorInfo& t = it->second;
+  if (!decodable(t.dtype))
+    return sfail(LTXW_ERR_UNSUPPORTED, "unsupported dtype %s for key \"%s\"", st::dtype_name(t.dtype), name);
+  if (n < 0 || (uint64_t)n != t.numel())
+    return sfail(LTXW_ERR_INVALID_ARG, "\"%s\" holds %llu elements, the buffer %lld", name,
+                 (unsigned long long)t.numel(), (long long)n);
+  if (n && !out) return sfail(LTXW_ERR_INVALID_ARG, "null output buffer");
+  decode_host(f->d->file->base + t.begin, t.dtype, (uint64_t)n, out);
+  return LTXW_OK;
+}
+
+int ltxw_store_merge_lora(ltxw_store* s, const ltxw_lora_file* f, float strength, ltxw_merge_report** report) {
+  if (report) *report = nullptr;
+  if (!s || !f) return sfail(LTXW_ERR_INVALID_ARG, "null store or LoRA file");
+  const LoraData& L = *f->d;
+  static const std::string kA = ".lora_A.weight";
+  std::unique_ptr<ltxw_merge_report> rep(new ltxw_merge_report());
+  std::vector<std::pair<std::string, Delta>> pending;
+  for (const std::string& key_a : L.names) {  // store.rs:549-560
+    if (!ends_with(key_a, kA)) continue;
+    const std::string prefix = key_a.substr(0, key_a.size() - kA.size());
+    const std::string base = prefix + ".weight", key_b = prefix + ".lora_B.weight";
+    auto be = s->entries.find(base);
+    if (be == s->entries.end()) {
+      rep->unmatched.push_back(key_a);
+      continue;
+    }
+    const st::TensorInfo& ta = L.tensors.at(key_a);
+    if (!decodable(ta.dtype))
+      return sfail(LTXW_ERR_UNSUPPORTED, "unsupported dtype %s for key \"%s\"", st::dtype_name(ta.dtype), key_a.c_str());
+    auto tb_it = L.tensors.find(key_b);
+    if (tb_it == L.tensors.end()) {
+      rep->unmatched.push_back(key_a);
+      continue;
+    }
+    const st::TensorInfo& tb = tb_it->second;
+    if (!decodable(tb.dtype))
+      return sfail(LTXW_ERR_UNSUPPORTED, "unsupported dtype %s for key \"%s\"", st::dtype_name(tb.dtype), key_b.c_str());
+    // store.rs:578-603
+    const uint64_t rank_a = dim_or(ta.shape, 0, 0), rank_b = dim_or(tb.shape, 1, 0);
+    if (rank_a != rank_b || rank_a == 0)
+      return sfail(LTXW_ERR_LORA_RANK, "LoRA inner rank mismatch for key \"%s\": A inner %llu, B inner %llu",
+                   base.c_str(), (unsigned long long)rank_a, (unsigned long long)rank_b);
+    const uint64_t out_f = dim_or(be->second.shape, 0, 0), in_f = dim_or(be->second.shape, 1, 1);
+    if (dim_or(tb.shape, 0, 0) != out_f || dim_or(ta.shape, 1, 0) != in_f)
+      return sfail(LTXW_ERR_LORA_SHAPE, "LoRA shape mismatch for key \"%s\"", base.c_str());
+    // store.rs:605-615: alpha defaults to rank; coeff = strength.mul_add(alpha / rank, 0).
+    float alpha = rank_f32(rank_a);
+    auto al = L.tensors.find(prefix + ".alpha");
+    if (al != L.tensors.end()) {
+      if (!decodable(al->second.dtype))
+        return sfail(LTXW_ERR_UNSUPPORTED, "unsupported dtype %s for key \"%s.alpha\"",
+                     st::dtype_name(al->second.dtype), prefix.c_str());
+      if (al->second.numel() > 0) decode_host(L.file->base + al->second.begin, al->second.dtype, 1, &alpha);
+    }
+    const float coeff = std::fma(strength, alpha / rank_f32(rank_a), 0.0f);
+    pending.emplace_back(base, Delta{f->d, key_a, key_b, rank_a, out_f, in_f, coeff});
+    rep->matched.push_back(base);
+  }
+  if (rep->matched.empty() && !rep->unmatched.empty())
+    return sfail(LTXW_ERR_NO_LORA_MATCHES, "LoRA file did not match any base weight keys");
+  for (auto& pd : pending) s->deltas[pd.first].push_back(std::move(pd.second));
+  std::sort(rep->matched.begin(), rep->matched.end());
+  std::sort(rep->unmatched.begin(), rep->unmatched.end());
+  if (report) *report = rep.release();
+  return LTXW_OK;
+}
+
+int64_t ltxw_report_n_matched(const ltxw_merge_report* r) { return r ? (int64_t)r->matched.size() : 0; }
+const char* ltxw_report_matched(const ltxw_merge_report* r, int64_t i) {
+  return (r && i >= 0 && i < (int64_t)r->matched.size()) ? r->matched[(size_t)i].c_str() : nullptr;
+}
+int64_t ltxw_report_n_unmatched(const ltxw_merge_report* r) { return r ? (int64_t)r->unmatched.size() : 0; }
+const char* ltxw_report_unmatched(const ltxw_merge_report* r, int64_t i) {
+  return (r && i >= 0 && i < (int64_t)r->unmatched.size()) ? r->unmatched[(size_t)i].c_str() : nullptr;
+}
+void ltxw_report_free(ltxw_merge_report* r) { delete r; }
+
+int ltxw_store_n_deltas(const ltxw_store* s, const char* key) {
+  if (!s || !key) return 0;
+  auto it = s->deltas.find(key);
+  return it == s->deltas.end() ? 0 : (int)it->second.size();
+}
+
+int ltxw_store_delta(const ltxw_store* s, const char* key, int index, int32_t* rank, float* coeff) {
+  if (!s || !key) return sfail(LTXW_ERR_INVALID_ARG, "null store or key");
+  auto it = s->deltas.find(key);
+  if (it == s->deltas.end() || index < 0 || index >= (int)it->second.size())
+    return sfail(LTXW_ERR_INVALID_ARG, "key \"%s\" has no delta %d", key, index);
+  const Delta& d = it->second[(size_t)index];
+  if (rank) *rank = d.rank > INT32_MAX ? INT32_MAX : (int32_t)d.rank;
+  if (coeff) *coeff = d.coeff;
+  return LTXW_OK;
+}
+
+int ltxw_store_materialize(ltxw_store* s, ltxw_ctx* ctx, const char* const* keys, int64_t n_keys,
+                           int32_t out_dtype, uint32_t flags, void* const* outs) {
+  return materialize(s, ctx, keys, n_keys, out_dtype, flags, outs);
+}
+
+int ltxw_store_read(ltxw_store* s, ltxw_ctx* ctx, const char* key, uint32_t flags, float* out, int64_t n) {
+  if (!s || !ctx || !key) return sfail(LTXW_ERR_INVALID_ARG, "null store, context or key");
+  auto it = s->entries.find(key);
+  if (it == s->entries.end()) return sfail(LTXW_ERR_MISSING_KEY, "missing key: \"%s\"", key);
+  const uint64_t numel = it->second.numel;
+  if (n < 0 || (uint64_t)n != numel)
+    return sfail(LTXW_ERR_INVALID_ARG, "\"%s\" holds %llu elements, the buffer %lld", key,
+                 (unsigned long long)numel, (long long)n);
+  if (numel == 0) {  // validate the key as `read` would, nothing to compute
+    void* none = nullptr;
+    return materialize(s, ctx, &key, 1, LTXW_OUT_F32, flags, &none);
+  }
+  if (!out) return sfail(LTXW_ERR_INVALID_ARG, "null output buffer");
+  void* dev = nullptr;
+  if (int rc = ltxw_alloc(ctx, numel * 4, &dev)) return sfail(rc, "%s", ltxw_last_error(ctx));
+  int rc = materialize(s, ctx, &key, 1, LTXW_OUT_F32, flags, &dev);
+  if (rc == LTXW_OK && (rc = ltxw_download(ctx, dev, numel * 4, out)) != LTXW_OK)
+    sfail(rc, "%s", ltxw_last_error(ctx));
+  int rf = ltxw_free(ctx, dev);
+  if (rc == LTXW_OK && rf != LTXW_OK) rc = sfail(rf, "%s", ltxw_last_error(ctx));
+  return rc;
+}
+
+}  // extern "C"

@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(os.path.dirname(_HERE), "_build", "libltxw.so")
 
 # include/ltxw.h enums
 OK = 0
-FMT_E4M3FN, FMT_E5M2 = 0, 1
+FMT_E4M3FN, FMT_E5M2, FMT_BF16, FMT_F16, FMT_F32 = 0, 1, 2, 3, 4
 SCALE_NONE, SCALE_TENSOR, SCALE_ROW = 0, 1, 2
 OUT_BF16, OUT_F32 = 0, 1
 MAX_LORAS = 4
@@ -75,12 +75,17 @@ _ERRORS = {c.code: c for c in (InvalidArgument, UnsupportedDtype, OutOfMemory, D
                                LoraRankMismatch, NoLoraMatches)}
 
 
+FACTOR_BF16, FACTOR_F32, FACTOR_F16, FACTOR_E4M3FN, FACTOR_E5M2 = 0, 1, 2, 3, 4
+
+
 class Lora(ctypes.Structure):
     _fields_ = [
         ("b", ctypes.c_void_p),
         ("a", ctypes.c_void_p),
         ("rank", ctypes.c_int32),
         ("coeff", ctypes.c_float),
+        ("dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 
@@ -99,10 +104,26 @@ class TensorDesc(ctypes.Structure):
     ]
 
 
+class KeyRule(ctypes.Structure):
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("n", ctypes.c_int32),
+        ("strs", ctypes.POINTER(ctypes.c_char_p)),
+    ]
+
+
 EXPORTS = [
     "ltxw_ctx_create", "ltxw_ctx_destroy", "ltxw_last_error", "ltxw_alloc", "ltxw_free",
     "ltxw_memset", "ltxw_upload", "ltxw_download", "ltxw_synchronize", "ltxw_dequant",
-    "ltxw_dequant_lora", "ltxw_dequant_lora_grouped", "ltxw_ctx_stream",
+    "ltxw_dequant_lora", "ltxw_dequant_lora_grouped", "ltxw_ctx_stream", "ltxw_ctx_set_host_threads",
+    # include/ltxw_store.h
+    "ltxw_store_last_error", "ltxw_store_open", "ltxw_store_close", "ltxw_store_n_keys",
+    "ltxw_store_key", "ltxw_store_contains", "ltxw_store_tensor_info", "ltxw_store_metadata",
+    "ltxw_lora_open", "ltxw_lora_close", "ltxw_lora_n_tensors", "ltxw_lora_tensor_name",
+    "ltxw_lora_tensor_info", "ltxw_lora_metadata", "ltxw_lora_ic_layout", "ltxw_lora_read_f32",
+    "ltxw_store_merge_lora", "ltxw_report_n_matched", "ltxw_report_matched", "ltxw_report_n_unmatched",
+    "ltxw_report_unmatched", "ltxw_report_free", "ltxw_store_n_deltas", "ltxw_store_delta",
+    "ltxw_store_materialize", "ltxw_store_read",
 ]
 
 _lib = None
@@ -133,8 +154,61 @@ def lib():
     L.ltxw_dequant_lora_grouped.argtypes = [vp, ctypes.POINTER(TensorDesc), i32]
     L.ltxw_ctx_stream.argtypes = [vp]
     L.ltxw_ctx_stream.restype = vp
+    L.ltxw_ctx_set_host_threads.argtypes = [vp, i32]
+    # include/ltxw_store.h
+    cp, u32, f32 = ctypes.c_char_p, ctypes.c_uint32, ctypes.c_float
+    pi32, pi64 = ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int64)
+    L.ltxw_store_last_error.argtypes = []
+    L.ltxw_store_last_error.restype = cp
+    L.ltxw_store_open.argtypes = [ctypes.POINTER(cp), i32, ctypes.POINTER(KeyRule), i32, ctypes.POINTER(vp)]
+    L.ltxw_store_close.argtypes = [vp]
+    L.ltxw_store_close.restype = None
+    L.ltxw_store_n_keys.argtypes = [vp]
+    L.ltxw_store_n_keys.restype = i64
+    L.ltxw_store_key.argtypes = [vp, i64]
+    L.ltxw_store_key.restype = cp
+    L.ltxw_store_contains.argtypes = [vp, cp]
+    L.ltxw_store_tensor_info.argtypes = [vp, cp, pi32, pi32, pi64, i32]
+    L.ltxw_store_metadata.argtypes = [vp, cp]
+    L.ltxw_store_metadata.restype = cp
+    L.ltxw_lora_open.argtypes = [cp, ctypes.POINTER(vp)]
+    L.ltxw_lora_close.argtypes = [vp]
+    L.ltxw_lora_close.restype = None
+    L.ltxw_lora_n_tensors.argtypes = [vp]
+    L.ltxw_lora_n_tensors.restype = i64
+    L.ltxw_lora_tensor_name.argtypes = [vp, i64]
+    L.ltxw_lora_tensor_name.restype = cp
+    L.ltxw_lora_tensor_info.argtypes = [vp, cp, pi32, pi32, pi64, i32]
+    L.ltxw_lora_metadata.argtypes = [vp, cp]
+    L.ltxw_lora_metadata.restype = cp
+    L.ltxw_lora_ic_layout.argtypes = [vp, ctypes.POINTER(u32), ctypes.POINTER(u32)]
+    L.ltxw_lora_read_f32.argtypes = [vp, cp, vp, i64]
+    L.ltxw_store_merge_lora.argtypes = [vp, vp, f32, ctypes.POINTER(vp)]
+    L.ltxw_report_n_matched.argtypes = [vp]
+    L.ltxw_report_n_matched.restype = i64
+    L.ltxw_report_matched.argtypes = [vp, i64]
+    L.ltxw_report_matched.restype = cp
+    L.ltxw_report_n_unmatched.argtypes = [vp]
+    L.ltxw_report_n_unmatched.restype = i64
+    L.ltxw_report_unmatched.argtypes = [vp, i64]
+    L.ltxw_report_unmatched.restype = cp
+    L.ltxw_report_free.argtypes = [vp]
+    L.ltxw_report_free.restype = None
+    L.ltxw_store_n_deltas.argtypes = [vp, cp]
+    L.ltxw_store_delta.argtypes = [vp, cp, i32, pi32, ctypes.POINTER(f32)]
+    L.ltxw_store_materialize.argtypes = [vp, vp, ctypes.POINTER(cp), i64, i32, u32, ctypes.POINTER(vp)]
+    L.ltxw_store_read.argtypes = [vp, vp, cp, u32, vp, i64]
     _lib = L
     return L
+
+
+def check_store(rc):
+    """Raise the WeightError subclass of a failed store / LoRA-file call."""
+    if rc == OK:
+        return
+    msg = lib().ltxw_store_last_error()
+    msg = msg.decode("utf-8", "replace") if msg else ""
+    raise _ERRORS.get(rc, WeightError)(msg)
 
 
 def check(rc, ctx_handle=None):
@@ -195,12 +269,15 @@ class Context:
     def stream(self):
         return lib().ltxw_ctx_stream(self.h)
 
+    def set_host_threads(self, n):
+        self._chk(lib().ltxw_ctx_set_host_threads(self.h, n))
+
     def dequant(self, w, rows, cols, fmt, scale_mode, scales, out, out_dtype=OUT_BF16):
         self._chk(lib().ltxw_dequant(self.h, w, rows, cols, fmt, scale_mode, scales, out, out_dtype))
 
     def dequant_lora(self, w, rows, cols, fmt, scale_mode, scales, loras, out, out_dtype=OUT_BF16):
-        """loras: list of (b_ptr, a_ptr, rank, coeff)."""
-        arr = (Lora * max(1, len(loras)))(*[Lora(b, a, r, c) for (b, a, r, c) in loras])
+        """loras: list of (b_ptr, a_ptr, rank, coeff[, factor_dtype])."""
+        arr = (Lora * max(1, len(loras)))(*[Lora(*x) for x in loras])
         self._chk(lib().ltxw_dequant_lora(self.h, w, rows, cols, fmt, scale_mode, scales, arr,
                                           len(loras), out, out_dtype))
 
@@ -215,6 +292,6 @@ class Context:
             t.out_dtype = d.get("out_dtype", OUT_BF16)
             loras = d.get("loras", [])
             t.n_loras = len(loras)
-            for l, (b, a, r, c) in enumerate(loras[:MAX_LORAS]):
-                t.loras[l] = Lora(b, a, r, c)
+            for l, x in enumerate(loras[:MAX_LORAS]):
+                t.loras[l] = Lora(*x)
         self._chk(lib().ltxw_dequant_lora_grouped(self.h, arr, len(descs)))

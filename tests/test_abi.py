@@ -1,5 +1,5 @@
 """CPU checks of the C ABI boundary: the library loads, exports every entry
-point include/ltxw.h declares, and reports a missing device as an error."""
+point the headers in include/ declare, and reports a missing device as an error."""
 import ctypes
 import os
 import re
@@ -12,15 +12,22 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def declared_entry_points():
-    with open(os.path.join(ROOT, "include", "ltxw.h")) as f:
-        text = f.read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(ltxw_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    inc = os.path.join(ROOT, "include")
+    for h in sorted(os.listdir(inc)):
+        if not h.endswith(".h"):
+            continue
+        with open(os.path.join(inc, h)) as f:
+            text = f.read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(ltxw_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_declares_the_entry_points():
     names = declared_entry_points()
     assert "ltxw_dequant" in names and "ltxw_dequant_lora" in names and "ltxw_dequant_lora_grouped" in names
+    assert "ltxw_store_open" in names and "ltxw_store_materialize" in names and "ltxw_store_merge_lora" in names
 
 
 def test_library_exports_every_declared_symbol():
@@ -51,3 +58,17 @@ def test_null_context_calls_fail_cleanly():
     assert L.ltxw_dequant(None, None, 1, 1, 0, 0, None, None, 0) == lw.InvalidArgument.code
     assert L.ltxw_ctx_stream(None) is None
     L.ltxw_ctx_destroy(None)
+
+
+def test_null_store_calls_fail_cleanly():
+    L = lw.lib()
+    assert L.ltxw_store_n_keys(None) == 0 and L.ltxw_store_key(None, 0) is None
+    assert L.ltxw_store_contains(None, b"x") == 0 and L.ltxw_store_metadata(None, b"x") is None
+    assert L.ltxw_store_materialize(None, None, None, 0, 0, 0, None) == lw.InvalidArgument.code
+    assert L.ltxw_store_read(None, None, b"x", 0, None, 0) == lw.InvalidArgument.code
+    assert L.ltxw_store_merge_lora(None, None, ctypes.c_float(1.0), None) == lw.InvalidArgument.code
+    assert L.ltxw_lora_open(None, None) == lw.InvalidArgument.code
+    assert L.ltxw_store_last_error()
+    L.ltxw_store_close(None)
+    L.ltxw_lora_close(None)
+    L.ltxw_report_free(None)

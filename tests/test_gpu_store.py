@@ -1,0 +1,304 @@
+"""GPU tests of the weight store: `read` and `materialize` through
+include/ltxw_store.h against the oracle and the reference's own expected
+values (crates/ltx-weights/tests/integration.rs).
+
+Bars: dequant (no LoRA) and every path that runs in the reference's
+operation order (non-bf16 factors, non-FP8 bases) bit-exact in f32 and bf16;
+bf16 factors on FP8 bases (MFMA path) within 1 bf16 ulp + the Frobenius
+bound of gpu_util.compare_lora_bf16.
+"""
+import numpy as np
+import pytest
+
+import gpu_util as U
+import ltx_weights as lw
+import oracle_lib as O
+import st_io
+from ltx_weights import synth
+from ltx_weights.store import MAT_SCALE_FIRST, KeyMap, LoraFile, WeightStore
+
+pytestmark = pytest.mark.gpu
+
+
+def log(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    log("test_gpu_store: context on device 0")
+    c = lw.Context(0)
+    yield c
+    c.close()
+
+
+@pytest.fixture
+def tmp(tmp_path):
+    class W:
+        n = 0
+
+        def __call__(self, tensors, metadata=None):
+            W.n += 1
+            p = tmp_path / f"g{W.n}.safetensors"
+            st_io.write(p, tensors, metadata)
+            return p
+
+    return W()
+
+
+def f32(*v):
+    return np.array(v, dtype=np.float32)
+
+
+def bits(x):
+    return np.asarray(x, dtype=np.float32).view(np.uint32)
+
+
+# ---------------------------------------------------------------------------
+# The reference's integration tests, through the device read path
+# ---------------------------------------------------------------------------
+def test_identity_reads_f32_f16_bf16(ctx, tmp):
+    log("identity reads")
+    vals = f32(0.5, 1.0, -1.0, 2.0)
+    bf = synth.bf16_from_f64([3.14, -2.71, 0.0, 1.0])
+    p = tmp([("f", "F32", [2, 2], f32(1, 2, 3, 4)), ("h", "F16", [4], vals.astype(np.float16).view(np.uint16)),
+             ("b", "BF16", [4], bf)])
+    s = WeightStore.open([p])
+    assert s.read("f", ctx)[1].tolist() == [[1, 2], [3, 4]]
+    assert np.array_equal(s.read("h", ctx)[1], vals)
+    assert np.array_equal(bits(s.read("b", ctx)[1]), bits(O.decode(bf, O.BF16)))
+
+
+def test_fp8_with_and_without_scale(ctx, tmp):
+    log("fp8 scale")
+    p = tmp([("w", "F8_E4M3", [1], np.array([0x38], np.uint8)), ("v", "F8_E4M3", [1], np.array([0x38], np.uint8)),
+             ("v_scale", "F32", [1], f32(3.0))])
+    s = WeightStore.open([p])
+    assert s.read("w", ctx)[1].tolist() == [1.0]
+    assert s.read("v", ctx)[1].tolist() == [3.0]
+
+
+def test_non_fp8_scale_sibling_not_applied(ctx, tmp):
+    p = tmp([("w", "F32", [1], f32(2.0)), ("w_scale", "F32", [1], f32(100.0))])
+    s = WeightStore.open([p])
+    assert s.read("w", ctx)[1].tolist() == [2.0]
+    assert s.read("w_scale", ctx)[1].tolist() == [100.0]
+
+
+def test_lora_merge_basic_alpha_and_stacking_values(ctx, tmp):
+    log("lora merge values")
+    base = tmp([("layer.weight", "F32", [2, 2], f32(1, 0, 0, 1)), ("w.weight", "F32", [2, 2], f32(0, 0, 0, 0)),
+                ("s.weight", "F32", [2, 2], f32(1, 0, 0, 1))])
+    store = WeightStore.open([base])
+    store.merge_lora(LoraFile.open(tmp([("layer.lora_A.weight", "F32", [1, 2], f32(1, 2)),
+                                        ("layer.lora_B.weight", "F32", [2, 1], f32(3, 4)),
+                                        ("w.lora_A.weight", "F32", [1, 2], f32(1, 2)),
+                                        ("w.lora_B.weight", "F32", [2, 1], f32(3, 4)),
+                                        ("w.alpha", "F32", [1], f32(2.0)),
+                                        ("s.lora_A.weight", "F32", [1, 2], f32(1, 2)),
+                                        ("s.lora_B.weight", "F32", [2, 1], f32(3, 4))])), 1.0)
+    store.merge_lora(LoraFile.open(tmp([("s.lora_A.weight", "F32", [2, 2], f32(1, 0, 0, 1)),
+                                        ("s.lora_B.weight", "F32", [2, 2], f32(2, 0, 0, -2))])), 0.5)
+    assert store.read("layer.weight", ctx)[1].tolist() == [[4, 6], [4, 9]]
+    assert store.read("w.weight", ctx)[1].tolist() == [[6, 12], [8, 16]]
+    assert store.read("s.weight", ctx)[1].tolist() == [[5, 6], [4, 8]]
+
+
+def test_read_errors(ctx, tmp):
+    p = tmp([("w", "I32", [2], np.array([42, -1], np.int32)), ("x", "F32", [1], f32(0))])
+    s = WeightStore.open([p])
+    with pytest.raises(lw.UnsupportedDtype):
+        s.read("w", ctx)
+    with pytest.raises(lw.MissingKey):
+        s.read("does_not_exist", ctx)
+
+
+# ---------------------------------------------------------------------------
+# Random cases against the oracle
+# ---------------------------------------------------------------------------
+FACTOR_DT = {"F32": O.F32, "F16": O.F16, "BF16": O.BF16, "F8_E4M3": O.E4M3FN, "F8_E5M2": O.E5M2}
+
+
+def factor_bits(rng, dt, shape, std):
+    x = rng.normal(0.0, std, size=shape)
+    if dt == "F32":
+        return x.astype(np.float32)
+    if dt == "F16":
+        return x.astype(np.float16).view(np.uint16)
+    if dt == "BF16":
+        return synth.bf16_from_f64(x)
+    codes = synth.E4M3FN_CODES if dt == "F8_E4M3" else synth.E5M2_FINITE_CODES
+    return codes[rng.integers(0, len(codes), size=shape)]
+
+
+def base_bits(rng, dt, shape):
+    if dt in ("F8_E4M3", "F8_E5M2"):
+        codes = synth.E4M3FN_CODES if dt == "F8_E4M3" else synth.E5M2_FINITE_CODES
+        return codes[rng.integers(0, len(codes), size=shape)]
+    return factor_bits(rng, dt, shape, 1.0)
+
+
+@pytest.mark.parametrize("base_dt,factor_dt,ranks,shape,scale", [
+    ("F8_E4M3", "F32", [3], (24, 40), "row"),
+    ("F8_E5M2", "F16", [5, 2], (33, 17), "tensor"),
+    ("F8_E4M3", "F8_E4M3", [4], (16, 16), "row"),
+    ("BF16", "BF16", [8], (20, 64), None),
+    ("F16", "F32", [2], (9, 31), None),
+    ("F32", "BF16", [16, 8], (12, 48), None),
+    ("F8_E4M3", "BF16", [6], (10, 30), "tensor"),   # cols % 8 != 0: generic path
+])
+def test_reference_order_paths_bit_exact(ctx, tmp, base_dt, factor_dt, ranks, shape, scale):
+    """Every path that keeps the reference's operation order matches the
+    oracle's f32 bit for bit (and its bf16 rounding)."""
+    log("reference-order case", base_dt, factor_dt, ranks, shape, scale)
+    rng = np.random.default_rng(hash((base_dt, factor_dt, tuple(ranks), shape)) % (1 << 31))
+    rows, cols = shape
+    w = base_bits(rng, base_dt, (rows, cols))
+    ts = [("t.weight", base_dt, [rows, cols], w)]
+    sc = None
+    if scale == "row":
+        sc = rng.uniform(1e-3, 1e-1, rows).astype(np.float32)
+        ts.append(("t.weight_scale", "F32", [rows], sc))
+    elif scale == "tensor":
+        sc = rng.uniform(1e-3, 1e-1, 1).astype(np.float32)
+        ts.append(("t.weight_scale", "F32", [], sc))
+    store = WeightStore.open([tmp(ts)])
+    loras = []
+    for k, r in enumerate(ranks):
+        a = factor_bits(rng, factor_dt, (r, cols), 0.05)
+        b = factor_bits(rng, factor_dt, (rows, r), 0.05)
+        strength = [1.0, 0.5, 0.25][k]
+        store.merge_lora(LoraFile.open(tmp([("t.lora_A.weight", factor_dt, [r, cols], a),
+                                            ("t.lora_B.weight", factor_dt, [rows, r], b)])), strength)
+        loras.append((b.reshape(rows, r), a.reshape(r, cols), FACTOR_DT[factor_dt], O.lora_coeff(strength, None, r)))
+    smode = {None: O.SCALE_NONE, "row": O.SCALE_ROW, "tensor": O.SCALE_TENSOR}[scale]
+    want = O.read_f32(w.reshape(rows, cols), O.DTYPE_CODES[base_dt], smode, sc, loras)
+    got = store.read("t.weight", ctx)[1]
+    assert np.array_equal(bits(got), bits(want))
+    # bf16 materialisation of the same key = RNE of that f32.
+    out = store.materialize_bf16(ctx, ["t.weight"])["t.weight"]
+    try:
+        assert np.array_equal(out.to_numpy(), O.read_bf16(w.reshape(rows, cols), O.DTYPE_CODES[base_dt], smode, sc,
+                                                          loras))
+    finally:
+        out.free()
+
+
+def test_fused_path_through_store(ctx, tmp):
+    log("fused through store")
+    rng = np.random.default_rng(11)
+    case = synth.tensor_case(11, 256, 512, synth.E5M2, synth.SCALE_ROW, loras=((64, 1.0), (32, 0.5)))
+    ts = [("m.weight", "F8_E5M2", [256, 512], case["w"]), ("m.weight_scale", "F32", [256], case["scales"])]
+    store = WeightStore.open([tmp(ts)])
+    for k, (b, a, r, c) in enumerate(case["loras"]):
+        store.merge_lora(LoraFile.open(tmp([("m.lora_A.weight", "BF16", [r, 512], a),
+                                            ("m.lora_B.weight", "BF16", [256, r], b)])), c)
+    out = store.materialize_bf16(ctx, ["m.weight"])["m.weight"]
+    try:
+        stats = U.compare_lora_bf16(case, out.to_numpy())
+    finally:
+        out.free()
+    log("fused via store:", stats)
+    del rng
+
+
+def test_scale_policy_and_dtypes(ctx, tmp):
+    """[rows] scales are per row by default and element 0 under the
+    reference's rule (LTXW_MAT_SCALE_FIRST); scales in bf16/f16 widen exactly."""
+    log("scale policy")
+    rng = np.random.default_rng(4)
+    rows, cols = 16, 64
+    w = synth.E4M3FN_CODES[rng.integers(0, 254, (rows, cols))]
+    s16 = synth.bf16_from_f64(rng.uniform(1e-3, 1e-1, rows))
+    store = WeightStore.open([tmp([("w", "F8_E4M3", [rows, cols], w), ("w_scale", "BF16", [rows], s16)])])
+    sc = O.decode(s16, O.BF16)
+    got_row = store.read("w", ctx)[1]
+    assert np.array_equal(bits(got_row), bits(O.read_f32(w, O.E4M3FN, O.SCALE_ROW, sc)))
+    got_first = store.read("w", ctx, flags=MAT_SCALE_FIRST)[1]
+    assert np.array_equal(bits(got_first), bits(O.read_f32(w, O.E4M3FN, O.SCALE_TENSOR, sc[:1])))
+    # A scale of another length scales by element 0 (store.rs:732-735).
+    store2 = WeightStore.open([tmp([("w", "F8_E4M3", [rows, cols], w),
+                                    ("w_scale", "F16", [3], np.array([0.5, 2, 4], np.float16).view(np.uint16))])])
+    assert np.array_equal(bits(store2.read("w", ctx)[1]), bits(O.read_f32(w, O.E4M3FN, O.SCALE_TENSOR, f32(0.5))))
+    # An empty scale tensor scales by 1.0 (and so turns -0 into +0).
+    neg0 = np.full((2, 8), 0x80, np.uint8)
+    store3 = WeightStore.open([tmp([("z", "F8_E4M3", [2, 8], neg0), ("z_scale", "F32", [0], np.zeros(0, np.float32))])])
+    assert np.all(bits(store3.read("z", ctx)[1]) == 0)
+
+
+def test_multidim_empty_and_errors(ctx, tmp):
+    log("multidim / empty / errors")
+    rng = np.random.default_rng(8)
+    w3 = synth.E4M3FN_CODES[rng.integers(0, 254, (4, 3, 5))]
+    p = tmp([("c", "F8_E4M3", [4, 3, 5], w3), ("e", "F32", [0, 7], np.zeros(0, np.float32)),
+             ("m.weight", "F32", [2, 3], np.zeros(6, np.float32))])
+    store = WeightStore.open([p])
+    got = store.read("c", ctx)[1]
+    assert got.shape == (4, 3, 5)
+    assert np.array_equal(bits(got).ravel(), bits(O.decode(w3.ravel(), O.E4M3FN)))
+    assert store.read("e", ctx)[1].shape == (0, 7)
+    # Five stacked LoRAs exceed the device path's limit of four.
+    for k in range(5):
+        store.merge_lora(LoraFile.open(tmp([("m.lora_A.weight", "F32", [1, 3], f32(1, 1, 1)),
+                                            ("m.lora_B.weight", "F32", [2, 1], f32(1, 1))])), 1.0)
+    with pytest.raises(lw.UnsupportedDtype):
+        store.read("m.weight", ctx)
+    with pytest.raises(lw.InvalidArgument):
+        store.materialize(ctx, ["c"], [None])
+    with pytest.raises(lw.MissingKey):
+        store.materialize(ctx, ["c", "nope"], [1 << 12, 1 << 12])
+
+
+# ---------------------------------------------------------------------------
+# A synthetic DiT checkpoint (mixed formats, edge shapes, two stacked LoRAs)
+# ---------------------------------------------------------------------------
+def test_synthetic_block_materialise_sampled_rows(ctx, tmp_path):
+    log("synthetic block: writing files")
+    m, l1, l2 = (tmp_path / n for n in ("m.safetensors", "l1.safetensors", "l2.safetensors"))
+    synth.write_model(m, 505, 1, variant=1, threads=8)
+    synth.write_lora(l1, 506, 1, 32, variant=1, threads=8)
+    synth.write_lora(l2, 507, 1, 128, variant=1, threads=8)
+    store = WeightStore.open([m], KeyMap.transformer())
+    store.merge_lora(LoraFile.open(l1), 1.0)
+    store.merge_lora(LoraFile.open(l2), 0.5)
+    layout = synth.model_layout(1, 1)
+    keys = [k for k, *_ in layout]
+    log("synthetic block: materialise", len(keys), "tensors")
+    outs = store.materialize_bf16(ctx, keys)
+    ctx.synchronize()
+    try:
+        for key, fmt, sm, r, c in layout:
+            rows = np.unique(np.array([0, 1, 2, r // 2, r - 2, r - 1]))
+            w, sc = synth.model_rows(505, key, fmt, sm, rows, c, r)
+            b1, a1 = synth.lora_factors_rows(506, key, 32, rows, r, c)
+            b2, a2 = synth.lora_factors_rows(507, key, 128, rows, r, c)
+            case = {"w": w, "scales": sc[rows] if sm == synth.SCALE_ROW else sc, "rows": len(rows), "cols": c,
+                    "fmt": fmt, "scale_mode": sm, "loras": [(b1, a1, 32, 1.0), (b2, a2, 128, 0.5)]}
+            got = outs[key].to_numpy()[rows]
+            stats = U.compare_lora_bf16(case, got)
+            log(key, stats["max_ulp"], round(stats["frob_vs_rne_f64"], 6))
+    finally:
+        for t in outs.values():
+            t.free()
+
+
+def test_repeated_materialise_is_stable(ctx, tmp):
+    """The staging and device rings are reused across calls: a second call
+    with different data in the same slots gives the right answer."""
+    log("repeated materialise")
+    rng = np.random.default_rng(21)
+    ts = []
+    for k in range(6):
+        w = synth.E4M3FN_CODES[rng.integers(0, 254, (128, 256))]
+        ts.append((f"k{k}.weight", "F8_E4M3", [128, 256], w))
+    store = WeightStore.open([tmp(ts)])
+    keys = [t[0] for t in ts]
+    for rep in range(3):
+        order = keys if rep % 2 == 0 else keys[::-1]
+        outs = store.materialize_bf16(ctx, order)
+        try:
+            for name, _, _, w in ts:
+                assert np.array_equal(outs[name].to_numpy(), O.read_bf16(w, O.E4M3FN)), (rep, name)
+        finally:
+            for t in outs.values():
+                t.free()
