@@ -107,9 +107,9 @@ typedef struct {
 typedef struct ltxw_ctx ltxw_ctx;
 
 /* Create a context on HIP device `device` with a ring of `n_staging` pinned
- * host buffers of `staging_bytes` each for host->device uploads (0 picks
- * 32 MiB x 16; allocated on first use). No reference counterpart: the
- * reference has no device. */
+ * host buffers of `staging_bytes` each (a multiple of 4096) for host->device
+ * uploads (0 picks 64 MiB x 16; one pinned block, allocated on first use).
+ * No reference counterpart: the reference has no device. */
 int ltxw_ctx_create(int device, size_t staging_bytes, int n_staging, ltxw_ctx** out);
 void ltxw_ctx_destroy(ltxw_ctx* ctx);
 

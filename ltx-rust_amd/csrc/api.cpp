@@ -305,29 +305,28 @@ int ltxw::run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n) {
 
 int ltxw::ensure_staging(ltxw_ctx* ctx) {
   if (!ctx->stage.empty()) return LTXW_OK;
+  // One contiguous pinned block, so that neighbouring slots can go out in a
+  // single copy.
+  void* block = nullptr;
+  const size_t total = ctx->stage_bytes * (size_t)ctx->n_stage;
+  if (hipHostMalloc(&block, total, hipHostMallocDefault) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(ctx, LTXW_ERR_OOM, "pinned staging ring of %zu bytes", total);
+  }
+  std::vector<hipEvent_t> evs;
   for (int k = 0; k < ctx->n_stage; ++k) {
-    void* p = nullptr;
     hipEvent_t ev = nullptr;
-    if (hipHostMalloc(&p, ctx->stage_bytes, hipHostMallocDefault) != hipSuccess) {
-      (void)hipGetLastError();
-      for (void* q : ctx->stage) (void)hipHostFree(q);
-      for (hipEvent_t e : ctx->stage_done) (void)hipEventDestroy(e);
-      ctx->stage.clear();
-      ctx->stage_done.clear();
-      return fail(ctx, LTXW_ERR_OOM, "pinned staging buffer of %zu bytes", ctx->stage_bytes);
-    }
-    ctx->stage.push_back(p);
     hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
     if (e != hipSuccess) {
-      ctx->stage_done.push_back(nullptr);
-      for (void* q : ctx->stage) (void)hipHostFree(q);
-      for (hipEvent_t x : ctx->stage_done) if (x) (void)hipEventDestroy(x);
-      ctx->stage.clear();
-      ctx->stage_done.clear();
+      for (hipEvent_t x : evs) (void)hipEventDestroy(x);
+      (void)hipHostFree(block);
       return hip_fail(ctx, e, "staging event");
     }
-    ctx->stage_done.push_back(ev);
+    evs.push_back(ev);
   }
+  ctx->stage_block = block;
+  for (int k = 0; k < ctx->n_stage; ++k) ctx->stage.push_back((char*)block + (size_t)k * ctx->stage_bytes);
+  ctx->stage_done = std::move(evs);
   ctx->next_stage = 0;
   return LTXW_OK;
 }
@@ -342,8 +341,10 @@ int ltxw_ctx_create(int device, size_t staging_bytes, int n_staging, ltxw_ctx** 
   if (e != hipSuccess) return fail(nullptr, LTXW_ERR_HIP, "hipGetDeviceCount: %s", hipGetErrorString(e));
   if (device < 0 || device >= ndev)
     return fail(nullptr, LTXW_ERR_INVALID_ARG, "device %d not in [0, %d)", device, ndev);
-  if (staging_bytes == 0) staging_bytes = 32u << 20;
+  if (staging_bytes == 0) staging_bytes = 64u << 20;
   if (n_staging <= 0) n_staging = 16;
+  if (staging_bytes % 4096 != 0)
+    return fail(nullptr, LTXW_ERR_INVALID_ARG, "staging_bytes %zu is not a multiple of 4096", staging_bytes);
   ltxw_ctx* c = new (std::nothrow) ltxw_ctx();
   if (!c) return fail(nullptr, LTXW_ERR_OOM, "context allocation");
   c->device = device;
@@ -375,7 +376,7 @@ void ltxw_ctx_destroy(ltxw_ctx* ctx) {
   (void)hipSetDevice(ctx->device);
   if (ctx->compute) (void)hipStreamSynchronize(ctx->compute);
   if (ctx->copy) (void)hipStreamSynchronize(ctx->copy);
-  for (void* p : ctx->stage) (void)hipHostFree(p);
+  if (ctx->stage_block) (void)hipHostFree(ctx->stage_block);
   for (hipEvent_t ev : ctx->stage_done) (void)hipEventDestroy(ev);
   for (void* p : ctx->ring) (void)hipFree(p);
   for (hipEvent_t ev : ctx->ring_free) (void)hipEventDestroy(ev);

@@ -15,9 +15,11 @@ struct ltxw_ctx {
   int host_threads = 8;
   hipStream_t compute = nullptr;
   hipStream_t copy = nullptr;
-  // Pinned staging ring for host -> device uploads (allocated on first use).
-  // Slot k may be refilled once stage_done[k] (recorded on the copy stream
-  // after the slot's last copy) has completed.
+  // Pinned staging ring for host -> device uploads (allocated on first use):
+  // n_stage slots of stage_bytes, consecutive in one block. Slot k may be
+  // refilled once stage_done[k] (recorded on the copy stream after the
+  // slot's last copy) has completed.
+  void* stage_block = nullptr;
   std::vector<void*> stage;
   std::vector<hipEvent_t> stage_done;
   size_t stage_bytes = 0;

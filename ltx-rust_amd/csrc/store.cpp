@@ -475,10 +475,19 @@ int ensure_ring(ltxw_ctx* ctx, uint64_t need) {
   return LTXW_OK;
 }
 
+// Host copy granularity: a staging slot is filled in sub-chunks of this size
+// by whichever host threads are free, so one slot fills at the threads'
+// combined rate.
+constexpr uint64_t kSubChunk = 8ull << 20;
+// Largest single host -> device copy: neighbouring filled slots that continue
+// one tensor segment go out as one copy (fewer, larger DMA transfers).
+constexpr uint64_t kMaxRun = 256ull << 20;
+
 // Staged pipeline over `plans` (each with numel > 0):
 //   host threads: mapped bytes -> pinned staging slot (slot p % S for piece p,
-//                 refilled once the copy of piece p - S has completed);
-//   this thread:  pinned slot -> device ring slot on the copy stream, in
+//                 refilled once the copy of piece p - S has completed), in
+//                 sub-chunks claimed in order;
+//   this thread:  filled slots -> device ring slot on the copy stream, in
 //                 piece order; after a batch's last piece, the compute stream
 //                 waits for the copies and runs the batch's kernels.
 // Host reads finish before return; device work completes in stream order.
@@ -527,6 +536,15 @@ int run_pipeline(ltxw_ctx* ctx, std::vector<Plan>& plans, int out_dtype) {
     batches.push_back(b);
   }
 
+  // Host copy work: (piece, offset) sub-chunks in piece order.
+  std::vector<std::pair<size_t, uint64_t>> chunks;
+  std::vector<std::atomic<int>> remaining(pieces.size());
+  for (size_t p = 0; p < pieces.size(); ++p) {
+    int n = 0;
+    for (uint64_t o = 0; o < pieces[p].len; o += kSubChunk, ++n) chunks.push_back({p, o});
+    remaining[p].store(n);
+  }
+
   // Shared state of the host copy threads.
   std::mutex mu;
   std::condition_variable cv;
@@ -540,8 +558,10 @@ int run_pipeline(ltxw_ctx* ctx, std::vector<Plan>& plans, int out_dtype) {
   auto worker = [&]() {
     (void)hipSetDevice(device);
     for (;;) {
-      const size_t p = next.fetch_add(1);
-      if (p >= pieces.size()) return;
+      const size_t c = next.fetch_add(1);
+      if (c >= chunks.size()) return;
+      const size_t p = chunks[c].first;
+      const uint64_t off = chunks[c].second, len = std::min(kSubChunk, pieces[p].len - off);
       const size_t s = p % S;
       {
         std::unique_lock<std::mutex> lk(mu);
@@ -557,15 +577,17 @@ int run_pipeline(ltxw_ctx* ctx, std::vector<Plan>& plans, int out_dtype) {
         cv.notify_all();
         return;
       }
-      memcpy(ctx->stage[s], pieces[p].src, pieces[p].len);
-      {
-        std::lock_guard<std::mutex> lk(mu);
-        filled[p] = 1;
+      memcpy((char*)ctx->stage[s] + off, pieces[p].src + off, len);
+      if (remaining[p].fetch_sub(1) == 1) {
+        {
+          std::lock_guard<std::mutex> lk(mu);
+          filled[p] = 1;
+        }
+        cv.notify_all();
       }
-      cv.notify_all();
     }
   };
-  const int nt = std::max(1, std::min<int>(ctx->host_threads, (int)pieces.size()));
+  const int nt = std::max(1, std::min<int>(ctx->host_threads, (int)chunks.size()));
   std::vector<std::thread> threads;
   threads.reserve((size_t)nt);
   for (int t = 0; t < nt; ++t) threads.emplace_back(worker);
@@ -581,7 +603,11 @@ int run_pipeline(ltxw_ctx* ctx, std::vector<Plan>& plans, int out_dtype) {
       rc = sfail(LTXW_ERR_HIP, "copy stream wait: %s", hipGetErrorString(he));
       break;
     }
-    for (size_t p = b.first_piece; p < b.end_piece; ++p) {
+    for (size_t p = b.first_piece; p < b.end_piece;) {
+      // Copy [p, q): piece p and the filled pieces that continue it in both
+      // the staging block (no wrap) and the device slot.
+      size_t q = p + 1;
+      uint64_t len = pieces[p].len;
       {
         std::unique_lock<std::mutex> lk(mu);
         cv.wait(lk, [&] { return abort || filled[p]; });
@@ -589,19 +615,27 @@ int run_pipeline(ltxw_ctx* ctx, std::vector<Plan>& plans, int out_dtype) {
           rc = sfail(LTXW_ERR_HIP, "%s", worker_err.c_str());
           break;
         }
+        while (q < b.end_piece && filled[q] && q % S != 0 && pieces[q - 1].len == stage &&
+               pieces[q].dst == pieces[q - 1].dst + stage && len + pieces[q].len <= kMaxRun) {
+          len += pieces[q].len;
+          ++q;
+        }
       }
-      const size_t s = p % S;
-      if ((he = hipMemcpyAsync(base + pieces[p].dst, ctx->stage[s], pieces[p].len, hipMemcpyHostToDevice,
-                               ctx->copy)) != hipSuccess ||
-          (he = hipEventRecord(ctx->stage_done[s], ctx->copy)) != hipSuccess) {
+      if ((he = hipMemcpyAsync(base + pieces[p].dst, ctx->stage[p % S], len, hipMemcpyHostToDevice, ctx->copy)) !=
+          hipSuccess) {
         rc = sfail(LTXW_ERR_HIP, "staged copy: %s", hipGetErrorString(he));
         break;
       }
+      for (size_t k = p; k < q && rc == LTXW_OK; ++k)
+        if ((he = hipEventRecord(ctx->stage_done[k % S], ctx->copy)) != hipSuccess)
+          rc = sfail(LTXW_ERR_HIP, "staged copy event: %s", hipGetErrorString(he));
+      if (rc) break;
       {
         std::lock_guard<std::mutex> lk(mu);
-        recorded = p + 1;
+        recorded = q;
       }
       cv.notify_all();
+      p = q;
     }
     if (rc) break;
     if ((he = hipEventRecord(ctx->ring_ready[slot], ctx->copy)) != hipSuccess ||
