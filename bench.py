@@ -39,8 +39,8 @@ HBM_PEAK_GBPS = 8000.0
 ROWS, COLS, RANK = 4096, 4096, 64
 ROTATE_BYTES = 1 << 30
 PMC_SUMMARY = {
-    "layer": os.path.join(ROOT, "profiles", "k_fused_layer4096x4096_r64.pmc.txt"),
-    "block": os.path.join(ROOT, "profiles", "k_fused_ditblock_r64.pmc.txt"),
+    "layer": os.path.join(ROOT, "profiles", "k_fused_pair_layer4096x4096_r64.pmc.txt"),
+    "block": os.path.join(ROOT, "profiles", "k_fused_pair_ditblock_r64.pmc.txt"),
 }
 
 
@@ -360,8 +360,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="layer", choices=sorted(WORKLOAD_TEXT))
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget (0 skips it)")
-    ap.add_argument("--e2e", default="model22b", choices=["none"] + sorted(MODEL_WORKLOADS),
-                    help="whole-model materialisation reported beside the kernel workload")
+    ap.add_argument("--e2e", default="auto", choices=["auto", "none"] + sorted(MODEL_WORKLOADS),
+                    help="whole-model materialisation reported beside the kernel workload "
+                         "(auto: the 22B set beside the default layer workload, none otherwise)")
     ap.add_argument("--e2e-steps", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -371,6 +372,8 @@ def main():
 
     if args.workload in MODEL_WORKLOADS:
         return main_model(args)
+    if args.e2e == "auto":
+        args.e2e = "model22b" if args.workload == "layer" else "none"
 
     import ltx_weights as lw
     from ltx_weights import synth

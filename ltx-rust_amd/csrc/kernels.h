@@ -73,8 +73,15 @@ hipError_t launch_dequant(const DequantArgs& a, int fmt, int scale_mode, bool f3
 
 // Fused dequant + LoRA over every work unit of every job. Requirements checked
 // by the caller: cols % 8 == 0, ranks % 8 == 0, all pointers 16-byte aligned,
-// total padded rank <= kRankMax.
+// total padded rank <= kRankMax, the same K-steps for every job
+// (lds_ld == 8 + 32 * K-steps). One workgroup per work unit when `multi`
+// (several LoRAs per tensor); one per pair of vertically adjacent units
+// (kPairRows rows) for single-LoRA tensors, and then unit_begin and
+// total_units count pairs.
 hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, hipStream_t stream);
+
+// Rows of one workgroup of the single-LoRA kernel.
+constexpr int kPairRows = 2 * kWavesPerGroup * kStripRows;
 
 // Padded K extent of one LoRA in the fused kernel's LDS stage.
 __host__ __device__ inline int pad_rank(int rank) { return (rank + 31) / 32 * 32; }

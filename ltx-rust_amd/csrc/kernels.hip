@@ -539,8 +539,9 @@ __device__ __forceinline__ void fused_unit(const JobDev& J, const LoraSteps& LS,
   }
 }
 
-// MULTI = false: exactly one LoRA. MULTI = true: 2..kMaxLoras LoRAs.
-// KS >= total K-steps of every job in the launch (register arrays are sized by it).
+// Launched with MULTI = true (2..kMaxLoras LoRAs per tensor; single-LoRA
+// tensors take k_fused_pair). KS = total K-steps of every job in the launch
+// (the host groups jobs by it).
 template <bool F32OUT, bool MULTI, int KS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MULTI ? 2 : 3))) void k_fused(JobTable tab) {
   extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
@@ -569,6 +570,291 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MULTI ? 2 :
   } else {
     if (full) fused_unit<F32OUT, MULTI, KS, true, 1>(J, LS, AT, tab.lds_ld, i0, g0, threadIdx.x);
     else fused_unit<F32OUT, MULTI, KS, false, 1>(J, LS, AT, tab.lds_ld, i0, g0, threadIdx.x);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// (b') Single-LoRA fused kernel: two vertically adjacent work units of one
+// band per workgroup, in straight-line code. A^T is staged once for both; the
+// second unit's FP8 bytes are requested with the first unit's, and its
+// L2-resident factor loads go out while the first unit's epilogue runs, so
+// the second unit's HBM latency hides behind the first unit's LoRA chain.
+// Per unit the arithmetic, layouts and stores are those of fused_unit.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t uni(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+template <typename T>
+__device__ __forceinline__ T* uni_ptr(T* p) {
+  const uint64_t v = (uint64_t)p;
+  return (T*)(((uint64_t)uni((uint32_t)(v >> 32)) << 32) | uni((uint32_t)v));
+}
+
+// The fields of one single-LoRA job the pipelined kernel uses, wave-uniform.
+struct PJ {
+  const uint8_t* w;
+  void* out;
+  const float* scales;
+  const uint16_t* a;
+  const uint16_t* b;
+  uint32_t rows, cols, rank, bands_n, scale_mode, fmt;
+  float coeff;
+  uint32_t unit_begin;
+};
+
+__device__ __forceinline__ PJ pj_load(const JobTable& t, uint64_t unit) {
+  JobDev J;
+  load_job(t, unit, J);
+  PJ p;
+  p.w = uni_ptr(J.w);
+  p.out = uni_ptr(J.out);
+  p.scales = uni_ptr(J.scales);
+  p.a = uni_ptr(J.lora[0].a);
+  p.b = uni_ptr(J.lora[0].b);
+  p.rows = uni((uint32_t)J.rows);
+  p.cols = uni((uint32_t)J.cols);
+  p.rank = uni((uint32_t)J.lora[0].rank);
+  p.bands_n = uni((uint32_t)J.bands_n);
+  p.scale_mode = uni((uint32_t)J.scale_mode);
+  p.fmt = uni((uint32_t)J.fmt);
+  p.coeff = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.lora[0].coeff)));
+  p.unit_begin = uni((uint32_t)J.unit_begin);
+  return p;
+}
+
+template <int KS>
+struct Frag {
+  bf16x8 bf[KS][2];
+  u32x2 wv[8];
+  float sc[8];
+};
+template <int KS>
+struct Stage {
+  u32x4 lo[KS], hi[KS];
+};
+
+template <int KS>
+__device__ __forceinline__ void pp_issue_a(const PJ& J, uint32_t i0, int tid, Stage<KS>& st) {
+  const int sq = tid & 15;
+  const uint32_t scol = i0 + 8 * (tid >> 4);
+  const bool scol_ok = scol < J.cols;
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    const uint32_t k = 32 * t + 2 * sq;
+    st.lo[t] = (u32x4){0u, 0u, 0u, 0u};
+    st.hi[t] = st.lo[t];
+    if (scol_ok && k < J.rank) st.lo[t] = ld_at<u32x4>(J.a, 2 * (k * J.cols + scol));
+    if (scol_ok && k + 1 < J.rank) st.hi[t] = ld_at<u32x4>(J.a, 2 * ((k + 1) * J.cols + scol));
+  }
+}
+
+template <int KS, bool FULL>
+__device__ __forceinline__ void pp_issue_f(const PJ& J, uint32_t i0, uint32_t g0, int tid, Frag<KS>& f) {
+  const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
+  const uint32_t rows = J.rows;
+  const uint32_t r0 = g0 + kStripRows * wave;
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    const uint32_t kk = 32 * t + 8 * lg;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const uint32_t ob = r0 + 16 * mb + ln;
+      f.bf[t][mb] = (bf16x8){};
+      if (kk < J.rank && (FULL || ob < rows)) f.bf[t][mb] = ld_at<bf16x8>(J.b, 2 * (ob * J.rank + kk));
+    }
+  }
+  const uint32_t rl = r0 + 4 * lg;
+  if (J.scale_mode == 2) {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const uint32_t rb = rl + 16 * mb;
+      if (FULL || rb + 3 < rows) {
+        const f32x4 q = ld_at<f32x4>(J.scales, 4 * rb);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) f.sc[4 * mb + v] = q[v];
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) f.sc[4 * mb + v] = rb + v < rows ? ld_at<float>(J.scales, 4 * (rb + v)) : 1.0f;
+      }
+    }
+  } else {
+    const float t = J.scale_mode == 1 ? ld_at<float>(J.scales, 0) : 1.0f;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) f.sc[g] = t;
+  }
+}
+
+template <int KS, bool FULL>
+__device__ __forceinline__ void pp_issue_w(const PJ& J, uint32_t i0, uint32_t g0, int tid, Frag<KS>& f) {
+  const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
+  const uint32_t rows = J.rows, cols = J.cols;
+  const uint32_t r0 = g0 + kStripRows * wave;
+  const uint32_t rl = r0 + 4 * lg;
+  const uint32_t ecol = i0 + 8 * ln;
+  const bool col_ok = FULL || ecol < cols;
+  const uint32_t e0 = rl * cols + ecol;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    const uint32_t dr = 16 * (g >> 2) + (g & 3);
+    f.wv[g] = (u32x2){0u, 0u};
+    if (col_ok && (FULL || rl + dr < rows)) f.wv[g] = ld_nt_at<u32x2>(J.w, e0 + dr * cols);
+  }
+}
+
+template <int KS>
+__device__ __forceinline__ void pp_stage(const Stage<KS>& st, uint16_t* AT, int ld, int tid) {
+  const int sq = tid & 15;
+#pragma unroll
+  for (int t = 0; t < KS; ++t)
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const uint32_t pair = __builtin_amdgcn_perm(st.hi[t][jj >> 1], st.lo[t][jj >> 1],
+                                                  (jj & 1) ? 0x07060302u : 0x05040100u);
+      *reinterpret_cast<uint32_t*>(&AT[(jj * 16 + (tid >> 4)) * ld + 32 * t + 2 * sq]) = pair;
+    }
+}
+
+template <int KS>
+struct Acc {
+  f32x4 v[2][8];
+};
+
+template <int KS>
+__device__ __forceinline__ void pp_mfma(const Frag<KS>& f, const uint16_t* AT, int ld, int tid, Acc<KS>& a) {
+  const int lane = tid & 63, ln = lane & 15, lg = lane >> 4;
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) a.v[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    const int kk = 32 * t + 8 * lg;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+      const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + kk]);
+      a.v[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][0], at, a.v[0][nb], 0, 0, 0);
+      a.v[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][1], at, a.v[1][nb], 0, 0, 0);
+    }
+  }
+}
+
+template <bool F32OUT, int KS, bool FULL, int FMT>
+__device__ __forceinline__ void pp_epilogue(const PJ& J, const Frag<KS>& f, Acc<KS>& a, uint32_t i0, uint32_t g0,
+                                            int tid) {
+  const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
+  const uint32_t rows = J.rows, cols = J.cols;
+  const uint32_t r0 = g0 + kStripRows * wave;
+  const float c = J.coeff;
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+    if (c != 1.0f) {
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) a.v[mb][nb] *= c;
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int g = 4 * mb + v;
+      float x[8];
+      decode4(f.wv[g][0], FMT, x);
+      decode4(f.wv[g][1], FMT, x + 4);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a.v[mb][j][v] = __builtin_fmaf(f.sc[g], x[j], a.v[mb][j][v]);
+    }
+  }
+  {
+    uint64_t any = 0;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) any |= __builtin_amdgcn_ballot_w64(__builtin_isnan(a.v[mb][nb][v]));
+    if (any) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) a.v[mb][nb][v] = canon_nan(a.v[mb][nb][v]);
+    }
+  }
+  const uint32_t rl = r0 + 4 * lg;
+  const uint32_t ecol = i0 + 8 * ln;
+  const bool col_ok = FULL || ecol < cols;
+  const uint32_t e0 = rl * cols + ecol;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    const int mb = g >> 2, v = g & 3;
+    const uint32_t dr = 16 * mb + v;
+    if (col_ok && (FULL || rl + dr < rows)) {
+      const uint32_t e = e0 + dr * cols;
+      float x[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = a.v[mb][j][v];
+      if (F32OUT) {
+        st_nt_at<f32x4>(J.out, 4 * e, (f32x4){x[0], x[1], x[2], x[3]});
+        st_nt_at<f32x4>(J.out, 4 * e + 16, (f32x4){x[4], x[5], x[6], x[7]});
+      } else {
+        const u32x4 o = {pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]), pack_bf16(x[4], x[5]), pack_bf16(x[6], x[7])};
+        st_nt_at<u32x4>(J.out, 2 * e, o);
+      }
+    }
+  }
+}
+
+template <bool F32OUT, int KS, int FMT>
+__device__ __forceinline__ void pp_epilogue_any(const PJ& J, const Frag<KS>& f, Acc<KS>& a, uint32_t i0,
+                                                uint32_t g0, int tid) {
+  if (g0 + 128 <= J.rows && i0 + 128 <= J.cols) pp_epilogue<F32OUT, KS, true, FMT>(J, f, a, i0, g0, tid);
+  else pp_epilogue<F32OUT, KS, false, FMT>(J, f, a, i0, g0, tid);
+}
+
+// Two vertically adjacent units of one band (rows [gA, gA + 256)).
+template <bool F32OUT, int KS, int FMT, bool FULL>
+__device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i0, uint32_t gA, uint32_t gB,
+                                           bool hasB, int tid) {
+  constexpr int LD = 32 * KS + 8;
+  Stage<KS> st;
+  pp_issue_a<KS>(J, i0, tid, st);
+  Frag<KS> fa, fb;
+  pp_issue_f<KS, FULL>(J, i0, gA, tid, fa);
+  pp_issue_w<KS, FULL>(J, i0, gA, tid, fa);
+  pp_issue_w<KS, FULL>(J, i0, hasB ? gB : gA, tid, fb);
+  pp_stage<KS>(st, AT, LD, tid);
+  __syncthreads();
+  {
+    Acc<KS> acc;
+    pp_mfma<KS>(fa, AT, LD, tid, acc);
+    pp_issue_f<KS, FULL>(J, i0, hasB ? gB : gA, tid, fb);
+    pp_epilogue<F32OUT, KS, FULL, FMT>(J, fa, acc, i0, gA, tid);
+  }
+  // Re-read the A^T fragments for the second unit rather than keeping them
+  // live (64 VGPRs) across the first unit's epilogue.
+  asm volatile("" ::: "memory");
+  if (hasB) {
+    Acc<KS> acc;
+    pp_mfma<KS>(fb, AT, LD, tid, acc);
+    pp_epilogue<F32OUT, KS, FULL, FMT>(J, fb, acc, i0, gB, tid);
+  }
+}
+
+// One workgroup per unit pair; the jobs' unit_begin count pairs.
+template <bool F32OUT, int KS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 3 : 2))) void k_fused_pair(JobTable tab) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
+  const int tid = threadIdx.x;
+  const uint32_t pair = xcd_remap(blockIdx.x, gridDim.x);
+  const PJ J = pj_load(tab, pair);
+  const uint32_t p = pair - J.unit_begin;
+  const uint32_t i0 = (p % J.bands_n) * kBandCols;
+  const uint32_t gA = (p / J.bands_n) * (2 * kWavesPerGroup * kStripRows);
+  const uint32_t gB = gA + kWavesPerGroup * kStripRows;
+  const bool hasB = gB < J.rows;
+  const bool full = gB + kWavesPerGroup * kStripRows <= J.rows && i0 + kBandCols <= J.cols;
+  if (J.fmt == 0) {
+    if (full) pair_units<F32OUT, KS, 0, true>(J, AT, i0, gA, gB, hasB, tid);
+    else pair_units<F32OUT, KS, 0, false>(J, AT, i0, gA, gB, hasB, tid);
+  } else {
+    if (full) pair_units<F32OUT, KS, 1, true>(J, AT, i0, gA, gB, hasB, tid);
+    else pair_units<F32OUT, KS, 1, false>(J, AT, i0, gA, gB, hasB, tid);
   }
 }
 
@@ -605,10 +891,10 @@ template <int KS>
 hipError_t launch_fused_ks(const JobTable& t, bool f32out, bool multi, dim3 grid, size_t lds, hipStream_t stream) {
   if (f32out) {
     if (multi) hipLaunchKernelGGL((k_fused<true, true, KS>), grid, dim3(256), lds, stream, t);
-    else hipLaunchKernelGGL((k_fused<true, false, KS>), grid, dim3(256), lds, stream, t);
+    else hipLaunchKernelGGL((k_fused_pair<true, KS>), grid, dim3(256), lds, stream, t);
   } else {
     if (multi) hipLaunchKernelGGL((k_fused<false, true, KS>), grid, dim3(256), lds, stream, t);
-    else hipLaunchKernelGGL((k_fused<false, false, KS>), grid, dim3(256), lds, stream, t);
+    else hipLaunchKernelGGL((k_fused_pair<false, KS>), grid, dim3(256), lds, stream, t);
   }
   return hipGetLastError();
 }
