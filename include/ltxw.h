@@ -38,7 +38,9 @@ typedef enum {
   LTXW_ERR_DUPLICATE_KEY = 8,  /* WeightError::DuplicateKey */
   LTXW_ERR_LORA_SHAPE = 9,     /* WeightError::LoraShapeMismatch */
   LTXW_ERR_LORA_RANK = 10,     /* WeightError::LoraRankMismatch */
-  LTXW_ERR_NO_LORA_MATCHES = 11 /* WeightError::NoLoraMatches */
+  LTXW_ERR_NO_LORA_MATCHES = 11, /* WeightError::NoLoraMatches */
+  LTXW_ERR_QKV_SPLIT_DIM = 12,   /* WeightError::QkvSplitDim */
+  LTXW_ERR_GATE_NOT_SCALAR = 13  /* WeightError::GateNotScalar */
 } ltxw_status;
 
 /* Base-weight storage formats: the FP8 formats of the hot path (safetensors

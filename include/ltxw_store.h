@@ -46,8 +46,20 @@ typedef enum {
   LTXW_RULE_DROP_PREFIX = 2,        /* n == 1: drop keys starting with strs[0] */
   LTXW_RULE_DROP_SUFFIX = 3,        /* n == 1: drop keys ending with strs[0] */
   LTXW_RULE_RENAME_EXACT = 4,       /* n == 2: a leading strs[0] becomes strs[1] */
-  /* Open-time value transforms (src/store.rs:217-390). Not built yet: a map
-   * holding one fails with LTXW_ERR_UNSUPPORTED. */
+  /* Open-time value transforms (n == 0), applied after renaming in this
+   * order whatever their position in the list (src/store.rs:190-198):
+   *   FOLD_GATES (src/store.rs:217-293): `.gate_msa/.gate_mlp/.gate_ctx`
+   *     scalars (else LTXW_ERR_GATE_NOT_SCALAR) multiply their targets
+   *     (`.attn.proj`, `.mlp.w_down`, `.context_proj` weight/bias) as
+   *     (v [* scale]) * gate in f32, plain multiplies; gates and the targets'
+   *     scale siblings disappear;
+   *   SPLIT_QKV (src/store.rs:302-390): `P.qkv.{weight,bias}` with leading dim
+   *     3d becomes `P.to_{q,k,v}.*` of leading dim d, FP8 scaled as `read`
+   *     would (leading dim not a multiple of 3: LTXW_ERR_QKV_SPLIT_DIM);
+   *   SYNTH_ZERO_TYPE_EMB (src/store.rs:398-419): a zero f32 `type_emb` of
+   *     conv_in.weight's dim 1 when absent.
+   * Transformed entries report dtype F32, as the reference's owned f32
+   * copies do; their values are computed on the device when read. */
   LTXW_RULE_SPLIT_QKV = 5,
   LTXW_RULE_FOLD_GATES = 6,
   LTXW_RULE_SYNTH_ZERO_TYPE_EMB = 7

@@ -177,11 +177,17 @@ bool fused_ok(const ltxw_tensor_desc& d) {
   return k <= ltxw::kRankMax;
 }
 
-int run_generic(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t begin, uint64_t count) {
+int run_generic(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t begin, uint64_t count,
+                const ltxw::DescEx* ex = nullptr) {
   ltxw::GenericArgs g{};
   g.job = to_job(d);
   g.elem_begin = begin;
   g.elem_count = count;
+  if (ex) {
+    g.plain_scale = ex->plain_scale;
+    g.has_post = ex->has_post;
+    g.post_mul = ex->post_mul;
+  }
   HIP_TRY(ctx, ltxw::launch_generic(g, d.out_dtype == LTXW_OUT_F32, ctx->compute), "generic kernel launch");
   return LTXW_OK;
 }
@@ -271,7 +277,7 @@ int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool 
 
 }  // namespace
 
-int ltxw::run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n) {
+int ltxw::run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n, const DescEx* ex) {
   // Validate everything before queuing anything.
   std::vector<uint64_t> counts((size_t)n);
   for (int k = 0; k < n; ++k) {
@@ -287,7 +293,9 @@ int ltxw::run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n) {
     uint64_t cnt = counts[(size_t)k];
     if (cnt == 0) continue;
     int rc = LTXW_OK;
-    if (d.n_loras == 0 && ltxw::format_bytes(d.fmt) == 1) {
+    if (ex && (ex[k].plain_scale || ex[k].has_post)) {
+      rc = run_generic(ctx, d, 0, cnt, &ex[k]);
+    } else if (d.n_loras == 0 && ltxw::format_bytes(d.fmt) == 1) {
       rc = run_dequant(ctx, d, cnt);
     } else if (fused_ok(d)) {
       ltxw::JobDev j = to_job(d);

@@ -53,9 +53,18 @@ int fail(ltxw_ctx* ctx, int code, const char* fmt, ...) __attribute__((format(pr
 // Allocates the pinned staging ring if it is not there yet.
 int ensure_staging(ltxw_ctx* ctx);
 
+// Per-descriptor extras of the store's open-time gate fold: scale as a plain
+// multiply, then a multiply by `post_mul` (before the LoRA deltas).
+struct DescEx {
+  int32_t plain_scale = 0;
+  int32_t has_post = 0;
+  float post_mul = 1.0f;
+};
+
 // Validates and queues the descriptors on the compute stream (the body of
-// ltxw_dequant_lora_grouped).
-int run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n);
+// ltxw_dequant_lora_grouped). `ex` (optional, n entries) routes descriptors
+// with extras to the reference-order kernel.
+int run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n, const DescEx* ex = nullptr);
 
 // Bytes per element of a base format (ltxw_format); 0 for an unknown one.
 inline int format_bytes(int fmt) {

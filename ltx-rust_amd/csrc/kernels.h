@@ -65,6 +65,12 @@ struct GenericArgs {
   JobDev job;
   uint64_t elem_begin;  // first flat element handled
   uint64_t elem_count;
+  // Open-time gate fold (store.rs:217-293): the scale as a plain multiply
+  // (v * s, keeping -0) instead of fma(s, v, 0), then v * post_mul, both
+  // before the LoRA deltas.
+  int32_t plain_scale;
+  int32_t has_post;
+  float post_mul;
 };
 
 // Streaming dequant: n_chunks * 16 elements. Pointers 16-byte aligned.

@@ -200,8 +200,11 @@ __global__ __launch_bounds__(256) void k_generic(GenericArgs g) {
   uint64_t cols = (uint64_t)J.cols;
   uint64_t o = e / cols, i = e % cols;
   float v = load_base(J, e);
-  if (J.scale_mode == 1) v = __builtin_fmaf(J.scales[0], v, 0.0f);
-  if (J.scale_mode == 2) v = __builtin_fmaf(J.scales[o], v, 0.0f);
+  if (J.scale_mode != 0) {
+    const float s = J.scales[J.scale_mode == 2 ? o : 0];
+    v = g.plain_scale ? s * v : __builtin_fmaf(s, v, 0.0f);
+  }
+  if (g.has_post) v = v * g.post_mul;
 #pragma unroll
   for (int l = 0; l < kMaxLoras; ++l) {
     if (l >= J.n_loras) break;

@@ -269,12 +269,27 @@ struct ltxw_merge_report {
 
 namespace {
 
+// Value transform of an entry made at open by the video-decoder key map
+// (store.rs:217-419); the reference materialises these eagerly as host f32.
+enum Xform : int32_t {
+  XF_NONE = 0,
+  XF_SPLIT = 1,  // QKV split part: the parent's bytes, scale as fma(s, v, 0) when has_scale
+  XF_GATE = 2,   // gate fold: (v [* scale]) * gate, plain multiplies
+  XF_OWNED = 3,  // host-owned f32 bytes (synthesised zero type_emb)
+};
+
 struct Entry {
-  int32_t dtype;
+  int32_t dtype;      // as reported (F32 for transformed entries, like the reference)
   std::vector<uint64_t> shape;
   uint32_t file;
-  uint64_t start, end;  // absolute in the file
+  uint64_t start, end;  // absolute in the file (unused for XF_OWNED)
   uint64_t numel;
+  int32_t src_dtype;   // element type of the stored bytes
+  int32_t xform = XF_NONE;
+  bool has_scale = false;
+  float scale = 1.0f;  // XF_SPLIT / XF_GATE
+  float gate = 1.0f;   // XF_GATE
+  std::shared_ptr<std::vector<uint8_t>> owned;  // XF_OWNED
 };
 
 // One merged low-rank delta (src/store.rs:751-763), kept as the adapter's
@@ -327,9 +342,12 @@ struct Plan {
   const uint8_t* fb[LTXW_MAX_LORAS];  // mapped factor bytes
   const uint8_t* fa[LTXW_MAX_LORAS];
   int fdt[LTXW_MAX_LORAS];            // ltxw_factor_dtype
+  ltxw::DescEx ex;                    // gate-fold extras
   // Offsets inside the batch's device slot.
   uint64_t off_w, off_s, off_b[LTXW_MAX_LORAS], off_a[LTXW_MAX_LORAS], bytes;
 };
+
+const uint8_t* entry_bytes(const ltxw_store* s, const Entry& e);
 
 int make_plan(const ltxw_store* s, const std::string& key, uint32_t flags, int out_dtype, void* out, Plan* p) {
   auto it = s->entries.find(key);
@@ -337,11 +355,11 @@ int make_plan(const ltxw_store* s, const std::string& key, uint32_t flags, int o
   const Entry& e = it->second;
   p->key = &it->first;
   p->e = &e;
-  p->wsrc = s->files[e.file]->base + e.start;
+  p->wsrc = entry_bytes(s, e);
   p->out = out;
-  p->fmt = device_format(e.dtype);
+  p->fmt = device_format(e.src_dtype);
   if (p->fmt < 0)
-    return sfail(LTXW_ERR_UNSUPPORTED, "unsupported dtype %s for key \"%s\"", st::dtype_name(e.dtype), key.c_str());
+    return sfail(LTXW_ERR_UNSUPPORTED, "unsupported dtype %s for key \"%s\"", st::dtype_name(e.src_dtype), key.c_str());
   p->esize = ltxw::format_bytes(p->fmt);
   p->numel = e.numel;
   p->rows = e.shape.empty() ? 1 : e.shape[0];
@@ -349,9 +367,20 @@ int make_plan(const ltxw_store* s, const std::string& key, uint32_t flags, int o
   if (p->numel && !out) return sfail(LTXW_ERR_INVALID_ARG, "null output buffer for key \"%s\"", key.c_str());
   (void)out_dtype;
 
-  // FP8 scale sibling (store.rs:498-508).
+  // FP8 scale sibling (store.rs:498-508), or the scale an open-time
+  // transform carried over from its source.
   p->scale_mode = LTXW_SCALE_NONE;
-  if (st::is_fp8(e.dtype)) {
+  if (e.xform == XF_SPLIT || e.xform == XF_GATE) {
+    if (e.has_scale) {
+      p->scales.assign(1, e.scale);
+      p->scale_mode = LTXW_SCALE_TENSOR;
+    }
+    if (e.xform == XF_GATE) {
+      p->ex.plain_scale = 1;
+      p->ex.has_post = 1;
+      p->ex.post_mul = e.gate;
+    }
+  } else if (st::is_fp8(e.dtype)) {
     auto sc = s->entries.find(key + "_scale");
     if (sc != s->entries.end()) {
       const Entry& se = sc->second;
@@ -594,6 +623,7 @@ int run_pipeline(ltxw_ctx* ctx, std::vector<Plan>& plans, int out_dtype) {
 
   int rc = LTXW_OK;
   std::vector<ltxw_tensor_desc> descs;
+  std::vector<ltxw::DescEx> exs;
   for (size_t bi = 0; bi < batches.size() && rc == LTXW_OK; ++bi) {
     const Batch& b = batches[bi];
     const size_t slot = bi % R;
@@ -644,6 +674,7 @@ int run_pipeline(ltxw_ctx* ctx, std::vector<Plan>& plans, int out_dtype) {
       break;
     }
     descs.clear();
+    exs.clear();
     for (size_t k = b.first_plan; k < b.first_plan + b.n_plans; ++k) {
       const Plan& p = plans[k];
       ltxw_tensor_desc d{};
@@ -660,8 +691,9 @@ int run_pipeline(ltxw_ctx* ctx, std::vector<Plan>& plans, int out_dtype) {
         d.loras[l] = {base + p.off_b[l], base + p.off_a[l], (int32_t)p.deltas[l]->rank, p.deltas[l]->coeff,
                       p.fdt[l], 0};
       descs.push_back(d);
+      exs.push_back(p.ex);
     }
-    if (int r2 = ltxw::run_descs(ctx, descs.data(), (int)descs.size())) {
+    if (int r2 = ltxw::run_descs(ctx, descs.data(), (int)descs.size(), exs.data())) {
       rc = sfail(r2, "%s", ctx->err.c_str());
       break;
     }
@@ -702,6 +734,156 @@ int materialize(ltxw_store* s, ltxw_ctx* ctx, const char* const* keys, int64_t n
 }  // namespace
 
 // ---------------------------------------------------------------------------
+// Open-time value transforms of the video-decoder key map.
+// ---------------------------------------------------------------------------
+namespace {
+
+// Gate-fold targets and their gates (key_map.rs:276-283).
+const char* const kGateTargets[][2] = {
+    {".attn.proj.weight", ".gate_msa"},   {".attn.proj.bias", ".gate_msa"},
+    {".mlp.w_down.weight", ".gate_mlp"},  {".mlp.w_down.bias", ".gate_mlp"},
+    {".context_proj.weight", ".gate_ctx"}, {".context_proj.bias", ".gate_ctx"},
+};
+const char* const kGateSuffixes[] = {".gate_msa", ".gate_mlp", ".gate_ctx"};
+
+const uint8_t* entry_bytes(const ltxw_store* s, const Entry& e) {
+  return e.xform == XF_OWNED ? e.owned->data() : s->files[e.file]->base + e.start;
+}
+
+// decode_scalar_f32 (store.rs:732-735): element 0, or 1.0 when empty.
+int scalar_of(const ltxw_store* s, const std::string& key, const Entry& e, float* v) {
+  if (!decodable(e.src_dtype))
+    return sfail(LTXW_ERR_UNSUPPORTED, "unsupported dtype %s for key \"%s\"", st::dtype_name(e.src_dtype), key.c_str());
+  *v = 1.0f;
+  if (e.numel) decode_host(entry_bytes(s, e), e.src_dtype, 1, v);
+  return LTXW_OK;
+}
+
+// store.rs:217-293. Gates must be scalars; every target with a gate becomes
+// f32 (v [* scale]) * gate, computed on the device at materialisation; the
+// target's scale sibling and the gate entries go away.
+int apply_gate_fold(ltxw_store* s) {
+  std::vector<std::string> gate_keys;
+  for (const auto& kv : s->entries)
+    for (const char* suf : kGateSuffixes)
+      if (ends_with(kv.first, suf)) gate_keys.push_back(kv.first);
+  std::unordered_map<std::string, float> gates;
+  for (const std::string& gk : gate_keys) {
+    const Entry& e = s->entries.at(gk);
+    const bool scalar = e.shape.empty() || (e.shape.size() == 1 && e.shape[0] == 1);
+    if (!scalar) {
+      std::string shp;
+      for (size_t k = 0; k < e.shape.size(); ++k) shp += (k ? ", " : "") + std::to_string(e.shape[k]);
+      return sfail(LTXW_ERR_GATE_NOT_SCALAR, "gate fold: expected scalar gate for key \"%s\", got shape [%s]",
+                   gk.c_str(), shp.c_str());
+    }
+    float g;
+    if (int rc = scalar_of(s, gk, e, &g)) return rc;
+    gates[gk] = g;
+  }
+  std::vector<std::string> params;
+  for (const auto& kv : s->entries) params.push_back(kv.first);
+  for (const std::string& pk : params) {
+    std::string gk;
+    for (const auto& t : kGateTargets)
+      if (ends_with(pk, t[0])) {
+        gk = pk.substr(0, pk.size() - strlen(t[0])) + t[1];
+        break;
+      }
+    if (gk.empty() || !gates.count(gk)) continue;
+    Entry& e = s->entries.at(pk);
+    if (!decodable(e.src_dtype) || e.xform != XF_NONE)
+      return sfail(LTXW_ERR_UNSUPPORTED, "unsupported dtype %s for key \"%s\"", st::dtype_name(e.src_dtype),
+                   pk.c_str());
+    if (st::is_fp8(e.src_dtype)) {
+      const std::string sk = pk + "_scale";
+      auto si = s->entries.find(sk);
+      if (si != s->entries.end()) {
+        float sc;
+        if (int rc = scalar_of(s, sk, si->second, &sc)) return rc;
+        e.has_scale = true;
+        e.scale = sc;
+      }
+      s->entries.erase(sk);
+      s->scale_keys.erase(sk);
+    }
+    e.xform = XF_GATE;
+    e.gate = gates[gk];
+    e.dtype = st::F32;
+  }
+  for (const std::string& gk : gate_keys) s->entries.erase(gk);
+  return LTXW_OK;
+}
+
+// store.rs:302-390. `P.qkv.{weight,bias}` with leading dim 3d becomes
+// P.to_q / P.to_k / P.to_v of leading dim d: each a contiguous third of the
+// parent's bytes, scaled (FP8) as the parent would be, reported as f32.
+int apply_qkv_split(ltxw_store* s) {
+  std::vector<std::string> keys;
+  for (const auto& kv : s->entries)
+    if (ends_with(kv.first, ".qkv.weight") || ends_with(kv.first, ".qkv.bias")) keys.push_back(kv.first);
+  std::sort(keys.begin(), keys.end());
+  for (const std::string& qk : keys) {
+    const Entry parent = s->entries.at(qk);
+    const uint64_t leading = parent.shape.empty() ? 0 : parent.shape[0];
+    if (leading % 3 != 0)
+      return sfail(LTXW_ERR_QKV_SPLIT_DIM, "QKV split: leading dim %llu for key \"%s\" is not divisible by 3",
+                   (unsigned long long)leading, qk.c_str());
+    if (!decodable(parent.src_dtype) || parent.xform != XF_NONE)
+      return sfail(LTXW_ERR_UNSUPPORTED, "unsupported dtype %s for key \"%s\"", st::dtype_name(parent.src_dtype),
+                   qk.c_str());
+    bool has_scale = false;
+    float sc = 1.0f;
+    const std::string sk = qk + "_scale";
+    if (st::is_fp8(parent.src_dtype)) {
+      auto si = s->entries.find(sk);
+      if (si != s->entries.end()) {
+        if (int rc = scalar_of(s, sk, si->second, &sc)) return rc;
+        has_scale = true;
+      }
+    }
+    const uint64_t per = parent.numel / 3;
+    const uint64_t esize = (uint64_t)st::dtype_bits(parent.src_dtype) / 8;
+    const bool weight = ends_with(qk, ".weight");
+    const std::string base = qk.substr(0, qk.rfind(".qkv."));
+    const char* parts[3] = {".to_q.", ".to_k.", ".to_v."};
+    for (int k = 0; k < 3; ++k) {
+      const std::string name = base + parts[k] + (weight ? "weight" : "bias");
+      if (s->entries.count(name)) return sfail(LTXW_ERR_DUPLICATE_KEY, "duplicate key \"%s\"", name.c_str());
+      Entry e = parent;
+      if (!e.shape.empty()) e.shape[0] = leading / 3;
+      e.numel = per;
+      e.start = parent.start + (uint64_t)k * per * esize;
+      e.end = e.start + per * esize;
+      e.xform = XF_SPLIT;
+      e.has_scale = has_scale;
+      e.scale = sc;
+      e.dtype = st::F32;
+      s->entries.emplace(name, std::move(e));
+    }
+    s->entries.erase(qk);
+    s->entries.erase(sk);
+    s->scale_keys.erase(sk);
+  }
+  return LTXW_OK;
+}
+
+// store.rs:398-419: a zero f32 `type_emb` of conv_in.weight's in-channels
+// when the checkpoint has none.
+void apply_zero_type_emb(ltxw_store* s) {
+  if (s->entries.count("type_emb")) return;
+  auto it = s->entries.find("conv_in.weight");
+  if (it == s->entries.end() || it->second.shape.size() < 2 || it->second.shape[1] == 0) return;
+  const uint64_t n = it->second.shape[1];
+  Entry e{st::F32, {n}, 0, 0, 0, n, st::F32};
+  e.xform = XF_OWNED;
+  e.owned = std::make_shared<std::vector<uint8_t>>(4 * n, 0);
+  s->entries.emplace("type_emb", std::move(e));
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
 // C ABI.
 // ---------------------------------------------------------------------------
 extern "C" {
@@ -715,6 +897,7 @@ int ltxw_store_open(const char* const* paths, int n_paths, const ltxw_key_rule* 
   if (n_paths < 0 || (n_paths > 0 && !paths) || n_rules < 0 || (n_rules > 0 && !rules))
     return sfail(LTXW_ERR_INVALID_ARG, "invalid path or rule array");
   std::vector<Rule> rs;
+  bool want_split = false, want_fold = false, want_type_emb = false;
   for (int k = 0; k < n_rules; ++k) {
     const ltxw_key_rule& r = rules[k];
     int want = -1;
@@ -724,10 +907,9 @@ int ltxw_store_open(const char* const* paths, int n_paths, const ltxw_key_rule* 
       case LTXW_RULE_RENAME_EXACT: want = 2; break;
       case LTXW_RULE_DROP_PREFIX:
       case LTXW_RULE_DROP_SUFFIX: want = 1; break;
-      case LTXW_RULE_SPLIT_QKV:
-      case LTXW_RULE_FOLD_GATES:
-      case LTXW_RULE_SYNTH_ZERO_TYPE_EMB:
-        return sfail(LTXW_ERR_UNSUPPORTED, "key rule %d (open-time value transform) is not supported", r.kind);
+      case LTXW_RULE_SPLIT_QKV: want_split = true; want = 0; break;
+      case LTXW_RULE_FOLD_GATES: want_fold = true; want = 0; break;
+      case LTXW_RULE_SYNTH_ZERO_TYPE_EMB: want_type_emb = true; want = 0; break;
       default: return sfail(LTXW_ERR_INVALID_ARG, "unknown key rule kind %d", r.kind);
     }
     if (r.n < 0 || (want >= 0 && r.n != want) || (r.n > 0 && !r.strs))
@@ -754,7 +936,7 @@ int ltxw_store_open(const char* const* paths, int n_paths, const ltxw_key_rule* 
       if (s->entries.count(name)) return sfail(LTXW_ERR_DUPLICATE_KEY, "duplicate key \"%s\" across checkpoint files",
                                                name.c_str());
       Entry e{t.second.dtype, t.second.shape, (uint32_t)s->files.size(), h.data_start + t.second.begin,
-              h.data_start + t.second.end, t.second.numel()};
+              h.data_start + t.second.end, t.second.numel(), t.second.dtype};
       s->entries.emplace(std::move(name), std::move(e));
     }
     s->files.push_back(std::move(f));
@@ -766,6 +948,12 @@ int ltxw_store_open(const char* const* paths, int n_paths, const ltxw_key_rule* 
     auto it = s->entries.find(k.substr(0, k.size() - 6));
     if (it != s->entries.end() && st::is_fp8(it->second.dtype)) s->scale_keys.insert(k);
   }
+  // Open-time value transforms, in the reference's order (store.rs:190-198).
+  if (want_fold)
+    if (int rc = apply_gate_fold(s.get())) return rc;
+  if (want_split)
+    if (int rc = apply_qkv_split(s.get())) return rc;
+  if (want_type_emb) apply_zero_type_emb(s.get());
   for (const auto& kv : s->entries)
     if (!s->scale_keys.count(kv.first)) s->visible.push_back(kv.first);
   std::sort(s->visible.begin(), s->visible.end());

@@ -31,6 +31,8 @@ from ._native import (  # noqa: F401
     LoraShapeMismatch,
     MissingKey,
     NoLoraMatches,
+    GateNotScalar,
+    QkvSplitDim,
     OutOfMemory,
     UnsupportedDtype,
     WeightError,

@@ -70,9 +70,17 @@ class NoLoraMatches(WeightError):
     code = 11
 
 
+class QkvSplitDim(WeightError):
+    code = 12
+
+
+class GateNotScalar(WeightError):
+    code = 13
+
+
 _ERRORS = {c.code: c for c in (InvalidArgument, UnsupportedDtype, OutOfMemory, DeviceError, IoError,
                                InvalidTensorData, MissingKey, DuplicateKey, LoraShapeMismatch,
-                               LoraRankMismatch, NoLoraMatches)}
+                               LoraRankMismatch, NoLoraMatches, QkvSplitDim, GateNotScalar)}
 
 
 FACTOR_BF16, FACTOR_F32, FACTOR_F16, FACTOR_E4M3FN, FACTOR_E5M2 = 0, 1, 2, 3, 4

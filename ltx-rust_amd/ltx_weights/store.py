@@ -58,6 +58,21 @@ class KeyMap:
                     (cls.REPLACE, ["vae.per_channel_statistics.", "per_channel_statistics."]),
                     (cls.REPLACE, ["encoder.", ""])])
 
+    @classmethod
+    def video_decoder(cls):
+        """`KeyMap::video_decoder` (src/key_map.rs:167-208), value transforms included."""
+        return cls([(cls.REQUIRE_ANY_PREFIX, ["vae.decoder.", "decoder.", "vae.per_channel_statistics.",
+                                              "per_channel_statistics."]),
+                    (cls.REPLACE, ["vae.decoder.", ""]),
+                    (cls.REPLACE, ["decoder.", ""]),
+                    (cls.REPLACE, ["vae.per_channel_statistics.", "per_channel_statistics."]),
+                    (cls.RENAME_EXACT, ["t_embedder.mlp.0.", "t_embedder.timestep_embedder.linear_1."]),
+                    (cls.RENAME_EXACT, ["t_embedder.mlp.2.", "t_embedder.timestep_embedder.linear_2."]),
+                    (cls.DROP_PREFIX, ["coarse_"]),
+                    (cls.FOLD_GATES, []),
+                    (cls.SPLIT_QKV, []),
+                    (cls.SYNTH_ZERO_TYPE_EMB, [])])
+
     def _c(self):
         keep = []
         arr = (N.KeyRule * max(1, len(self.rules)))()

@@ -302,3 +302,74 @@ def test_repeated_materialise_is_stable(ctx, tmp):
         finally:
             for t in outs.values():
                 t.free()
+
+
+# ---------------------------------------------------------------------------
+# Video-decoder value transforms (integration.rs:253-398)
+# ---------------------------------------------------------------------------
+def test_video_decoder_qkv_split_values(ctx, tmp):
+    log("qkv split values")
+    p = tmp([("vae.decoder.blocks.0.attn.qkv.weight", "F32", [3, 4], np.arange(12, dtype=np.float32))])
+    s = WeightStore.open([p], KeyMap.video_decoder())
+    assert s.read("blocks.0.attn.to_q.weight", ctx)[1].tolist() == [[0, 1, 2, 3]]
+    assert s.read("blocks.0.attn.to_k.weight", ctx)[1].tolist() == [[4, 5, 6, 7]]
+    assert s.read("blocks.0.attn.to_v.weight", ctx)[1].tolist() == [[8, 9, 10, 11]]
+    p = tmp([("vae.decoder.blocks.0.attn.qkv.weight", "F8_E4M3", [3, 1], np.array([0x38, 0x40, 0x44], np.uint8)),
+             ("vae.decoder.blocks.0.attn.qkv.weight_scale", "F32", [1], f32(4.0))])
+    s = WeightStore.open([p], KeyMap.video_decoder())
+    assert [s.read(f"blocks.0.attn.{x}.weight", ctx)[1].tolist() for x in ("to_q", "to_k", "to_v")] == [
+        [[4.0]], [[8.0]], [[12.0]]]
+
+
+def test_zero_type_emb_values(ctx, tmp):
+    p = tmp([("vae.decoder.conv_in.weight", "F32", [2, 3, 1], np.arange(6, dtype=np.float32))])
+    s = WeightStore.open([p], KeyMap.video_decoder())
+    assert s.read("type_emb", ctx)[1].tolist() == [0.0, 0.0, 0.0]
+
+
+def test_video_decoder_gate_fold_values(ctx, tmp):
+    log("gate fold values")
+    p = tmp([("vae.decoder.blocks.0.gate_msa", "F32", [1], f32(2.0)),
+             ("vae.decoder.blocks.0.attn.proj.weight", "F32", [2, 1], f32(1.0, 2.0)),
+             ("vae.decoder.blocks.0.attn.proj.bias", "F32", [2], f32(0.5, 1.5))])
+    s = WeightStore.open([p], KeyMap.video_decoder())
+    assert s.read("blocks.0.attn.proj.weight", ctx)[1].tolist() == [[2.0], [4.0]]
+    assert s.read("blocks.0.attn.proj.bias", ctx)[1].tolist() == [1.0, 3.0]
+    p = tmp([("vae.decoder.blocks.0.gate_msa", "F32", [1], f32(2.0)),
+             ("vae.decoder.blocks.0.attn.proj.weight", "F8_E4M3", [1], np.array([0x38], np.uint8)),
+             ("vae.decoder.blocks.0.attn.proj.weight_scale", "F32", [1], f32(4.0))])
+    s = WeightStore.open([p], KeyMap.video_decoder())
+    assert s.read("blocks.0.attn.proj.weight", ctx)[1].tolist() == [8.0]
+
+
+def test_transforms_bit_exact_random(ctx, tmp):
+    """Random FP8 / bf16 tensors through gate fold and QKV split, against the
+    reference's arithmetic restated in numpy f32 (plain multiplies for the
+    fold, fma(s, v, 0) for the split), with a LoRA merged onto a split part."""
+    log("transforms random")
+    rng = np.random.default_rng(17)
+    w8 = synth.E4M3FN_CODES[rng.integers(0, 254, (6, 40))]
+    w8[0, :4] = [0x80, 0x00, 0x7F, 0x01]  # -0, +0, NaN, subnormal
+    wb = synth.bf16_from_f64(rng.standard_normal((12, 8)))
+    s_scale, gate = np.float32(0.0371), np.float32(-1.75)
+    p = tmp([("vae.decoder.m.mlp.w_down.weight", "F8_E4M3", [6, 40], w8),
+             ("vae.decoder.m.mlp.w_down.weight_scale", "F32", [1], np.array([s_scale], np.float32)),
+             ("vae.decoder.m.gate_mlp", "F32", [], np.array([gate], np.float32)),
+             ("vae.decoder.m.attn.qkv.weight", "BF16", [12, 8], wb),
+             ("vae.decoder.n.attn.qkv.weight", "F8_E4M3", [6, 40], w8),
+             ("vae.decoder.n.attn.qkv.weight_scale", "F32", [1], np.array([s_scale], np.float32))])
+    store = WeightStore.open([p], KeyMap.video_decoder())
+    dec = O.decode(w8.ravel(), O.E4M3FN).reshape(6, 40)
+    want = (dec * s_scale).astype(np.float32) * gate
+    assert np.array_equal(bits(store.read("m.mlp.w_down.weight", ctx)[1]), bits(want.astype(np.float32)))
+    for k, part in enumerate(("to_q", "to_k", "to_v")):
+        got = store.read(f"m.attn.{part}.weight", ctx)[1]
+        assert np.array_equal(bits(got), bits(O.decode(wb[4 * k:4 * k + 4].ravel(), O.BF16).reshape(4, 8)))
+    # LoRA on a split FP8 part: the scaled FP8 base (fma(s, v, 0)) plus the delta, reference order.
+    a = rng.normal(0, 0.05, (3, 40)).astype(np.float32)
+    b = rng.normal(0, 0.05, (2, 3)).astype(np.float32)
+    store.merge_lora(LoraFile.open(tmp([("n.attn.to_k.lora_A.weight", "F32", [3, 40], a),
+                                        ("n.attn.to_k.lora_B.weight", "F32", [2, 3], b)])), 0.5)
+    want = O.read_f32(w8[2:4], O.E4M3FN, O.SCALE_TENSOR, np.array([s_scale], np.float32),
+                      [(b, a, O.F32, O.lora_coeff(0.5, None, 3))])
+    assert np.array_equal(bits(store.read("n.attn.to_k.weight", ctx)[1]), bits(want))

@@ -85,11 +85,82 @@ def test_empty_require_any_prefix_passes_all(tmp):
     assert WeightStore.open([p], KeyMap([(KeyMap.REQUIRE_ANY_PREFIX, [])])).keys() == ["k"]
 
 
-def test_value_transform_rules_are_reported_unsupported(tmp):
-    p = tmp([("k", "F32", [1], f32(1))])
-    for kind in (KeyMap.SPLIT_QKV, KeyMap.FOLD_GATES, KeyMap.SYNTH_ZERO_TYPE_EMB):
-        with pytest.raises(lw.UnsupportedDtype):
-            WeightStore.open([p], KeyMap([(kind, [])]))
+# ---------------------------------------------------------------------------
+# Video-decoder map: renames and open-time value transforms
+# (integration.rs:195-398, 831-848; the values are GPU tests)
+# ---------------------------------------------------------------------------
+def test_video_decoder_renames_and_drops(tmp):
+    p = tmp([("vae.decoder.conv_in.weight", "F32", [2, 1], f32(0.5, 1.0)),
+             ("vae.decoder.t_embedder.mlp.0.weight", "F32", [2, 1], f32(1, 2)),
+             ("vae.decoder.t_embedder.mlp.2.bias", "F32", [2], f32(1, 2)),
+             ("vae.decoder.coarse_up.weight", "F32", [1], f32(1)),
+             ("vae.per_channel_statistics.mean", "F32", [2], f32(1, 2)),
+             ("other.weight", "F32", [1], f32(1))])
+    s = WeightStore.open([p], KeyMap.video_decoder())
+    assert s.keys() == ["conv_in.weight", "per_channel_statistics.mean",
+                        "t_embedder.timestep_embedder.linear_1.weight",
+                        "t_embedder.timestep_embedder.linear_2.bias", "type_emb"]
+    # conv_in.weight [2, 1] -> a zero type_emb of 1 channel (store.rs:398-419).
+    assert s.shape("type_emb") == [1] and s.dtype("type_emb") == "F32"
+
+
+def test_type_emb_kept_when_present_or_no_conv_in(tmp):
+    p = tmp([("decoder.conv_in.weight", "F32", [1, 3], f32(1, 2, 3)), ("decoder.type_emb", "BF16", [2],
+                                                                         np.zeros(2, np.uint16))])
+    s = WeightStore.open([p], KeyMap.video_decoder())
+    assert s.shape("type_emb") == [2] and s.dtype("type_emb") == "BF16"
+    s = WeightStore.open([tmp([("decoder.x", "F32", [1], f32(1))])], KeyMap.video_decoder())
+    assert not s.contains("type_emb")
+
+
+def test_qkv_split_keys_shapes_and_scale_sibling(tmp):
+    p = tmp([("vae.decoder.blocks.0.attn.qkv.weight", "F8_E4M3", [3, 1], np.array([0x38, 0x40, 0x44], np.uint8)),
+             ("vae.decoder.blocks.0.attn.qkv.weight_scale", "F32", [1], f32(4.0)),
+             ("vae.decoder.blocks.0.attn.qkv.bias", "F32", [6], np.arange(6, dtype=np.float32))])
+    s = WeightStore.open([p], KeyMap.video_decoder())
+    assert not s.contains("blocks.0.attn.qkv.weight") and not s.contains("blocks.0.attn.qkv.weight_scale")
+    for part in ("to_q", "to_k", "to_v"):
+        assert s.shape(f"blocks.0.attn.{part}.weight") == [1, 1]
+        assert s.dtype(f"blocks.0.attn.{part}.weight") == "F32"
+        assert s.shape(f"blocks.0.attn.{part}.bias") == [2]
+    with pytest.raises(lw.MissingKey):
+        s.shape("blocks.0.attn.qkv.weight_scale")
+
+
+def test_qkv_split_bad_dim_and_duplicates(tmp):
+    p = tmp([("decoder.blocks.0.attn.qkv.weight", "F32", [5, 4], np.zeros(20, np.float32))])
+    with pytest.raises(lw.QkvSplitDim, match="leading dim 5"):
+        WeightStore.open([p], KeyMap.video_decoder())
+    p = tmp([("decoder.a.qkv.weight", "F32", [3, 1], f32(1, 2, 3)), ("decoder.a.to_k.weight", "F32", [1, 1], f32(9))])
+    with pytest.raises(lw.DuplicateKey):
+        WeightStore.open([p], KeyMap.video_decoder())
+
+
+def test_gate_fold_keys_and_errors(tmp):
+    p = tmp([("vae.decoder.blocks.0.gate_msa", "F32", [1], f32(2.0)),
+             ("vae.decoder.blocks.0.attn.proj.weight", "F8_E4M3", [1], np.array([0x38], np.uint8)),
+             ("vae.decoder.blocks.0.attn.proj.weight_scale", "F32", [1], f32(4.0)),
+             ("vae.decoder.blocks.0.attn.proj.bias", "F32", [2], f32(0.5, 1.5)),
+             ("vae.decoder.blocks.0.gate_mlp", "F32", [], f32(3.0))])  # no target: just removed
+    s = WeightStore.open([p], KeyMap.video_decoder())
+    assert s.keys() == ["blocks.0.attn.proj.bias", "blocks.0.attn.proj.weight"]
+    assert s.dtype("blocks.0.attn.proj.weight") == "F32" and s.dtype("blocks.0.attn.proj.bias") == "F32"
+    with pytest.raises(lw.MissingKey):
+        s.shape("blocks.0.attn.proj.weight_scale")
+    p = tmp([("decoder.b.gate_ctx", "F32", [2], f32(1, 2)), ("decoder.b.context_proj.weight", "F32", [1], f32(1))])
+    with pytest.raises(lw.GateNotScalar):
+        WeightStore.open([p], KeyMap.video_decoder())
+    p = tmp([("decoder.b.gate_msa", "I32", [1], np.array([2], np.int32)), ("decoder.b.attn.proj.bias", "F32", [1], f32(1))])
+    with pytest.raises(lw.UnsupportedDtype):
+        WeightStore.open([p], KeyMap.video_decoder())
+
+
+def test_value_transforms_run_only_when_asked(tmp):
+    p = tmp([("a.qkv.weight", "F32", [3, 1], f32(1, 2, 3)), ("a.gate_msa", "F32", [1], f32(2))])
+    assert WeightStore.open([p]).keys() == ["a.gate_msa", "a.qkv.weight"]
+    assert WeightStore.open([p], KeyMap([(KeyMap.SPLIT_QKV, [])])).keys() == [
+        "a.gate_msa", "a.to_k.weight", "a.to_q.weight", "a.to_v.weight"]
+    assert WeightStore.open([p], KeyMap([(KeyMap.FOLD_GATES, [])])).keys() == ["a.qkv.weight"]
 
 
 def test_fp8_scale_key_is_internal(tmp):
