@@ -236,13 +236,12 @@ int job_k(const ltxw::JobDev& j) {
 }
 
 // One fused launch over `jobs` (all fused_ok, same out dtype, multi flag and
-// K-steps): one workgroup per 128-column band and 128 rows (several LoRAs) or
-// 256 rows (one LoRA) of every job.
+// K-steps): one workgroup per 128-column band and 256 rows of every job.
 int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool multi) {
   if (jobs.empty()) return LTXW_OK;
   int kmax = 0;
   for (auto& j : jobs) kmax = std::max(kmax, job_k(j));
-  const int64_t group_rows = multi ? (int64_t)ltxw::kWavesPerGroup * ltxw::kStripRows : (int64_t)ltxw::kPairRows;
+  const int64_t group_rows = ltxw::kPairRows;
   int64_t units = 0;
   for (auto& j : jobs) {
     j.unit_begin = units;

@@ -80,10 +80,9 @@ hipError_t launch_dequant(const DequantArgs& a, int fmt, int scale_mode, bool f3
 // Fused dequant + LoRA over every work unit of every job. Requirements checked
 // by the caller: cols % 8 == 0, ranks % 8 == 0, all pointers 16-byte aligned,
 // total padded rank <= kRankMax, the same K-steps for every job
-// (lds_ld == 8 + 32 * K-steps). One workgroup per work unit when `multi`
-// (several LoRAs per tensor); one per pair of vertically adjacent units
-// (kPairRows rows) for single-LoRA tensors, and then unit_begin and
-// total_units count pairs.
+// (lds_ld == 8 + 32 * K-steps). One workgroup per pair of vertically
+// adjacent 128-row units (kPairRows rows); unit_begin and total_units count
+// pairs. `multi`: several LoRAs per tensor.
 hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, hipStream_t stream);
 
 // Rows of one workgroup of the single-LoRA kernel.

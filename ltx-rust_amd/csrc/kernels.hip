@@ -227,8 +227,8 @@ __global__ __launch_bounds__(256) void k_generic(GenericArgs g) {
 // ---------------------------------------------------------------------------
 // (b) Fused dequant + LoRA merge.
 //
-// Workgroup: 4 waves; work unit: one band of 128 output columns [i0, i0+128)
-// by 128 rows; wave w owns the strip of rows [r0, r0+32), r0 = 128*g + 32*w.
+// Work unit: one band of 128 output columns [i0, i0+128) by 128 rows; each of
+// a workgroup's 4 waves owns a strip of 32 rows, [r0, r0+32).
 //
 // LoRA product on v_mfma_f32_16x16x32_bf16 with M = output row o, N = output
 // column i, K = rank r, and the N index permuted as i = i0 + 8*n + nb for
@@ -320,269 +320,12 @@ __device__ __forceinline__ void st_nt_at(void* base, uint32_t off, T v) {
                                      (__attribute__((address_space(1))) char*)base + off));
 }
 
-// One work unit: rows [g0, g0 + 128) x columns [i0, i0 + 128) of job J.
-// FULL: the unit lies entirely inside the tensor (no bounds tests).
-// FMT: 0 = e4m3fn, 1 = e5m2 (J.fmt, resolved once per workgroup).
-template <bool F32OUT, bool MULTI, int KS, bool FULL, int FMT>
-__device__ __forceinline__ void fused_unit(const JobDev& J, const LoraSteps& LS, uint16_t* AT, int ld,
-                                           uint32_t i0, uint32_t g0, int tid) {
-  const int lane = tid & 63, wave = tid >> 6;
-  const int ln = lane & 15;  // MFMA column n / output column group
-  const int lg = lane >> 4;  // MFMA row group (rows 4*lg .. 4*lg+3 of an M-block)
-  const uint32_t rows = (uint32_t)J.rows, cols = (uint32_t)J.cols;
-  const uint32_t r0 = g0 + kStripRows * wave;
-  const uint32_t ecol = i0 + 8 * ln;
-  const bool col_ok = FULL || ecol < cols;
-
-  // 1. L2-resident factors: the A stage of every K-step, then the B fragments.
-  const int sq = tid & 15;
-  const uint32_t scol = i0 + 8 * (tid >> 4);
-  const bool scol_ok = FULL || scol < cols;
-  u32x4 st_lo[KS], st_hi[KS];
-#pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    st_lo[t] = (u32x4){0u, 0u, 0u, 0u};
-    st_hi[t] = st_lo[t];
-    if (t < LS.total) {
-      const StepInfo si = MULTI ? step_info(LS, t) : StepInfo{0, t, false};
-      const uint32_t k = 32 * si.kt + 2 * sq;
-#pragma unroll
-      for (int q = 0; q < (MULTI ? kMaxLoras : 1); ++q) {
-        if (si.l != q) continue;  // uniform; keeps J.lora indexed statically
-        const LoraDev& L = J.lora[q];
-        if (scol_ok && k < (uint32_t)L.rank) st_lo[t] = ld_at<u32x4>(L.a, 2 * (k * cols + scol));
-        if (scol_ok && k + 1 < (uint32_t)L.rank) st_hi[t] = ld_at<u32x4>(L.a, 2 * ((k + 1) * cols + scol));
-      }
-    }
-  }
-  bf16x8 bf[KS][2];
-#pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    bf[t][0] = (bf16x8){};
-    bf[t][1] = (bf16x8){};
-    if (t < LS.total) {
-      const StepInfo si = MULTI ? step_info(LS, t) : StepInfo{0, t, false};
-      const uint32_t kk = 32 * si.kt + 8 * lg;
-#pragma unroll
-      for (int q = 0; q < (MULTI ? kMaxLoras : 1); ++q) {
-        if (si.l != q) continue;
-        const LoraDev& L = J.lora[q];
-        const uint32_t rank = (uint32_t)L.rank;
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
-          const uint32_t ob = r0 + 16 * mb + ln;
-          if (kk < rank && (FULL || ob < rows)) bf[t][mb] = ld_at<bf16x8>(L.b, 2 * (ob * rank + kk));
-        }
-      }
-    }
-  }
-
-  // 2. HBM: this lane's FP8 bytes (8 rows x 8 columns) and their scales.
-  //    Group g = 4*mb + v is row r0 + 16*mb + 4*lg + v.
-  const uint32_t rl = r0 + 4 * lg;
-  const uint32_t e0 = rl * cols + ecol;  // element offset of group 0
-  u32x2 wv[8];
-#pragma unroll
-  for (int g = 0; g < 8; ++g) {
-    const uint32_t dr = 16 * (g >> 2) + (g & 3);
-    wv[g] = (u32x2){0u, 0u};
-    if (col_ok && (FULL || rl + dr < rows)) wv[g] = ld_nt_at<u32x2>(J.w, e0 + dr * cols);
-  }
-  float sc[8];
-  if (J.scale_mode == 2) {
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      const uint32_t rb = rl + 16 * mb;
-      if (FULL || rb + 3 < rows) {
-        const f32x4 q = ld_at<f32x4>(J.scales, 4 * rb);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) sc[4 * mb + v] = q[v];
-      } else {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) sc[4 * mb + v] = rb + v < rows ? ld_at<float>(J.scales, 4 * (rb + v)) : 1.0f;
-      }
-    }
-  } else {
-    const float t = J.scale_mode == 1 ? ld_at<float>(J.scales, 0) : 1.0f;
-#pragma unroll
-    for (int g = 0; g < 8; ++g) sc[g] = t;
-  }
-
-  // 3. LDS stage, then the MFMAs (their inputs are already in flight).
-#pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    if (t < LS.total) {
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        // (A[k][i], A[k+1][i]) for column i = scol + jj: the same half of word jj/2 of each row.
-        const uint32_t pair = __builtin_amdgcn_perm(st_hi[t][jj >> 1], st_lo[t][jj >> 1],
-                                                    (jj & 1) ? 0x07060302u : 0x05040100u);
-        *reinterpret_cast<uint32_t*>(&AT[(jj * 16 + (tid >> 4)) * ld + 32 * t + 2 * sq]) = pair;
-      }
-    }
-  }
-  __syncthreads();
-
-  f32x4 acc[2][8];
-  f32x4 delta[MULTI ? 2 : 1][MULTI ? 8 : 1];
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  // Epilogue values of M-block mb, in place of its accumulators:
-  //   y = fma(scale, decode(w), coeff * (B A)), scale = 1 when unscaled.
-  // (The reference rounds scale*decode(w) first; one rounding fewer here.)
-  auto epi_values = [&](int mb, float c) {
-    if (c != 1.0f) {  // uniform; the coefficient is 1 in the common case
-#pragma unroll
-      for (int nb = 0; nb < 8; ++nb) acc[mb][nb] *= c;
-    }
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int g = 4 * mb + v;
-      float x[8];
-      decode4(wv[g][0], FMT, x);
-      decode4(wv[g][1], FMT, x + 4);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[mb][j][v] = __builtin_fmaf(sc[g], x[j], acc[mb][j][v]);
-    }
-  };
-
-  if (!MULTI) {
-#pragma unroll
-    for (int t = 0; t < KS; ++t) {
-      if (t < LS.total) {
-        const int kk = 32 * t + 8 * lg;
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb) {
-          const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + kk]);
-          acc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[t][0], at, acc[0][nb], 0, 0, 0);
-          acc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[t][1], at, acc[1][nb], 0, 0, 0);
-        }
-      }
-    }
-    const float c = J.lora[0].coeff;
-    epi_values(0, c);
-    epi_values(1, c);
-  } else {
-#pragma unroll
-    for (int t = 0; t < KS; ++t) {
-      if (t < LS.total) {
-        const int kk = 32 * t + 8 * lg;
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb) {
-          const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + kk]);
-          acc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[t][0], at, acc[0][nb], 0, 0, 0);
-          acc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[t][1], at, acc[1][nb], 0, 0, 0);
-        }
-        // Last K-step of its LoRA: fold coeff * (B A) into the running sum.
-        const StepInfo si = step_info(LS, t);
-        if (si.last) {
-          float cl = J.lora[0].coeff;
-#pragma unroll
-          for (int q = 1; q < kMaxLoras; ++q)
-            if (si.l == q) cl = J.lora[q].coeff;
-          const bool first = si.l == 0;
-#pragma unroll
-          for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-            for (int nb = 0; nb < 8; ++nb) {
-#pragma unroll
-              for (int v = 0; v < 4; ++v)
-                delta[mb][nb][v] = first ? cl * acc[mb][nb][v] : __builtin_fmaf(cl, acc[mb][nb][v], delta[mb][nb][v]);
-              acc[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
-            }
-        }
-      }
-    }
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = delta[mb][nb];
-    epi_values(0, 1.0f);
-    epi_values(1, 1.0f);
-  }
-
-  // 4. Canonical NaNs (one wave-wide test), RNE to bf16, stores.
-  {
-    uint64_t any = 0;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < 8; ++nb)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) any |= __builtin_amdgcn_ballot_w64(__builtin_isnan(acc[mb][nb][v]));
-    if (any) {
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) acc[mb][nb][v] = canon_nan(acc[mb][nb][v]);
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < 8; ++g) {
-    const int mb = g >> 2, v = g & 3;
-    const uint32_t dr = 16 * mb + v;
-    if (col_ok && (FULL || rl + dr < rows)) {
-      const uint32_t e = e0 + dr * cols;
-      float x[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = acc[mb][j][v];
-      if (F32OUT) {
-        st_nt_at<f32x4>(J.out, 4 * e, (f32x4){x[0], x[1], x[2], x[3]});
-        st_nt_at<f32x4>(J.out, 4 * e + 16, (f32x4){x[4], x[5], x[6], x[7]});
-      } else {
-        const u32x4 o = {pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]), pack_bf16(x[4], x[5]), pack_bf16(x[6], x[7])};
-        st_nt_at<u32x4>(J.out, 2 * e, o);
-      }
-    }
-  }
-}
-
-// Launched with MULTI = true (2..kMaxLoras LoRAs per tensor; single-LoRA
-// tensors take k_fused_pair). KS = total K-steps of every job in the launch
-// (the host groups jobs by it).
-template <bool F32OUT, bool MULTI, int KS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MULTI ? 2 : 3))) void k_fused(JobTable tab) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
-  const uint64_t unit = xcd_remap(blockIdx.x, gridDim.x);
-  JobDev J;
-  load_job(tab, unit, J);
-  const uint64_t u = unit - (uint64_t)J.unit_begin;
-  const uint32_t i0 = (uint32_t)(u % (uint64_t)J.bands_n) * kBandCols;
-  const uint32_t g0 = (uint32_t)(u / (uint64_t)J.bands_n) * (kWavesPerGroup * kStripRows);
-  const int nl = MULTI ? J.n_loras : 1;
-  LoraSteps LS;
-  {
-    int k0 = 0;
-#pragma unroll
-    for (int l = 0; l < kMaxLoras; ++l) {
-      LS.kst[l] = k0;
-      LS.nks[l] = l < nl ? pad_rank(J.lora[l].rank) / 32 : 0;
-      k0 += LS.nks[l];
-    }
-    LS.total = k0;
-  }
-  const bool full = (int64_t)g0 + kWavesPerGroup * kStripRows <= J.rows && (int64_t)i0 + kBandCols <= J.cols;
-  if (J.fmt == 0) {
-    if (full) fused_unit<F32OUT, MULTI, KS, true, 0>(J, LS, AT, tab.lds_ld, i0, g0, threadIdx.x);
-    else fused_unit<F32OUT, MULTI, KS, false, 0>(J, LS, AT, tab.lds_ld, i0, g0, threadIdx.x);
-  } else {
-    if (full) fused_unit<F32OUT, MULTI, KS, true, 1>(J, LS, AT, tab.lds_ld, i0, g0, threadIdx.x);
-    else fused_unit<F32OUT, MULTI, KS, false, 1>(J, LS, AT, tab.lds_ld, i0, g0, threadIdx.x);
-  }
-}
-
 // ---------------------------------------------------------------------------
-// (b') Single-LoRA fused kernel: two vertically adjacent work units of one
-// band per workgroup, in straight-line code. A^T is staged once for both; the
-// second unit's FP8 bytes are requested with the first unit's, and its
-// L2-resident factor loads go out while the first unit's epilogue runs, so
-// the second unit's HBM latency hides behind the first unit's LoRA chain.
-// Per unit the arithmetic, layouts and stores are those of fused_unit.
+// (b') Workgroup schedule: two vertically adjacent work units of one band per
+// workgroup, in straight-line code. A^T is staged once for both; the second
+// unit's FP8 bytes are requested with the first unit's, and its L2-resident
+// factor loads go out while the first unit's epilogue runs, so the second
+// unit's HBM latency hides behind the first unit's LoRA chain.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t uni(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 template <typename T>
@@ -861,6 +604,203 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 3
   }
 }
 
+// ---------------------------------------------------------------------------
+// Several LoRAs per tensor, two units per workgroup. The LoRAs sit side by
+// side along K (each padded to 32); a LoRA's product is folded into the
+// running delta with its coefficient at the LoRA's last K-step:
+//   delta = c_0 (B_0 A_0) [+ c_1 (B_1 A_1) ...],  y = fma(scale, decode(w), delta).
+// ---------------------------------------------------------------------------
+struct PJM {
+  PJ base;  // coeff = 1: the delta already carries the coefficients
+  const uint16_t* a[kMaxLoras];
+  const uint16_t* b[kMaxLoras];
+  uint32_t rank[kMaxLoras];
+  float coeff[kMaxLoras];
+  LoraSteps ls;
+};
+
+__device__ __forceinline__ PJM pjm_load(const JobTable& t, uint64_t unit) {
+  JobDev J;
+  load_job(t, unit, J);
+  PJM m;
+  m.base.w = uni_ptr(J.w);
+  m.base.out = uni_ptr(J.out);
+  m.base.scales = uni_ptr(J.scales);
+  m.base.a = nullptr;
+  m.base.b = nullptr;
+  m.base.rows = uni((uint32_t)J.rows);
+  m.base.cols = uni((uint32_t)J.cols);
+  m.base.rank = 0;
+  m.base.bands_n = uni((uint32_t)J.bands_n);
+  m.base.scale_mode = uni((uint32_t)J.scale_mode);
+  m.base.fmt = uni((uint32_t)J.fmt);
+  m.base.coeff = 1.0f;
+  m.base.unit_begin = uni((uint32_t)J.unit_begin);
+  const int nl = (int)uni((uint32_t)J.n_loras);
+  int k0 = 0;
+#pragma unroll
+  for (int l = 0; l < kMaxLoras; ++l) {
+    m.a[l] = uni_ptr(J.lora[l].a);
+    m.b[l] = uni_ptr(J.lora[l].b);
+    m.rank[l] = uni((uint32_t)J.lora[l].rank);
+    m.coeff[l] = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.lora[l].coeff)));
+    m.ls.kst[l] = k0;
+    m.ls.nks[l] = l < nl ? pad_rank((int)m.rank[l]) / 32 : 0;
+    k0 += m.ls.nks[l];
+  }
+  m.ls.total = k0;
+  return m;
+}
+
+template <int KS>
+__device__ __forceinline__ void pm_issue_a(const PJM& M, uint32_t i0, int tid, Stage<KS>& st) {
+  const int sq = tid & 15;
+  const uint32_t cols = M.base.cols;
+  const uint32_t scol = i0 + 8 * (tid >> 4);
+  const bool scol_ok = scol < cols;
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    const StepInfo si = step_info(M.ls, t);
+    const uint32_t k = 32 * si.kt + 2 * sq;
+    st.lo[t] = (u32x4){0u, 0u, 0u, 0u};
+    st.hi[t] = st.lo[t];
+#pragma unroll
+    for (int q = 0; q < kMaxLoras; ++q) {
+      if (si.l != q) continue;  // uniform; keeps the arrays indexed statically
+      if (scol_ok && k < M.rank[q]) st.lo[t] = ld_at<u32x4>(M.a[q], 2 * (k * cols + scol));
+      if (scol_ok && k + 1 < M.rank[q]) st.hi[t] = ld_at<u32x4>(M.a[q], 2 * ((k + 1) * cols + scol));
+    }
+  }
+}
+
+template <int KS, bool FULL>
+__device__ __forceinline__ void pm_issue_f(const PJM& M, uint32_t g0, int tid, Frag<KS>& f) {
+  const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
+  const uint32_t rows = M.base.rows;
+  const uint32_t r0 = g0 + kStripRows * wave;
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    const StepInfo si = step_info(M.ls, t);
+    const uint32_t kk = 32 * si.kt + 8 * lg;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) f.bf[t][mb] = (bf16x8){};
+#pragma unroll
+    for (int q = 0; q < kMaxLoras; ++q) {
+      if (si.l != q) continue;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const uint32_t ob = r0 + 16 * mb + ln;
+        if (kk < M.rank[q] && (FULL || ob < rows)) f.bf[t][mb] = ld_at<bf16x8>(M.b[q], 2 * (ob * M.rank[q] + kk));
+      }
+    }
+  }
+  const uint32_t rl = r0 + 4 * lg;
+  if (M.base.scale_mode == 2) {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const uint32_t rb = rl + 16 * mb;
+      if (FULL || rb + 3 < rows) {
+        const f32x4 q = ld_at<f32x4>(M.base.scales, 4 * rb);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) f.sc[4 * mb + v] = q[v];
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          f.sc[4 * mb + v] = rb + v < rows ? ld_at<float>(M.base.scales, 4 * (rb + v)) : 1.0f;
+      }
+    }
+  } else {
+    const float t = M.base.scale_mode == 1 ? ld_at<float>(M.base.scales, 0) : 1.0f;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) f.sc[g] = t;
+  }
+}
+
+template <int KS>
+__device__ __forceinline__ void pm_mfma(const PJM& M, const Frag<KS>& f, const uint16_t* AT, int ld, int tid,
+                                        Acc<KS>& delta) {
+  const int lane = tid & 63, ln = lane & 15, lg = lane >> 4;
+  f32x4 acc[2][8];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    const int kk = 32 * t + 8 * lg;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+      const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + kk]);
+      acc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][0], at, acc[0][nb], 0, 0, 0);
+      acc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][1], at, acc[1][nb], 0, 0, 0);
+    }
+    const StepInfo si = step_info(M.ls, t);
+    if (si.last) {
+      float cl = M.coeff[0];
+#pragma unroll
+      for (int q = 1; q < kMaxLoras; ++q)
+        if (si.l == q) cl = M.coeff[q];
+      const bool first = si.l == 0;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            delta.v[mb][nb][v] = first ? cl * acc[mb][nb][v] : __builtin_fmaf(cl, acc[mb][nb][v], delta.v[mb][nb][v]);
+          acc[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        }
+    }
+  }
+}
+
+template <bool F32OUT, int KS, int FMT, bool FULL>
+__device__ __forceinline__ void pair_units_multi(const PJM& M, uint16_t* AT, uint32_t i0, uint32_t gA, uint32_t gB,
+                                                 bool hasB, int tid) {
+  constexpr int LD = 32 * KS + 8;
+  Stage<KS> st;
+  pm_issue_a<KS>(M, i0, tid, st);
+  Frag<KS> fa, fb;
+  pm_issue_f<KS, FULL>(M, gA, tid, fa);
+  pp_issue_w<KS, FULL>(M.base, i0, gA, tid, fa);
+  pp_issue_w<KS, FULL>(M.base, i0, hasB ? gB : gA, tid, fb);
+  pp_stage<KS>(st, AT, LD, tid);
+  __syncthreads();
+  {
+    Acc<KS> delta;
+    pm_mfma<KS>(M, fa, AT, LD, tid, delta);
+    pm_issue_f<KS, FULL>(M, hasB ? gB : gA, tid, fb);
+    pp_epilogue<F32OUT, KS, FULL, FMT>(M.base, fa, delta, i0, gA, tid);
+  }
+  asm volatile("" ::: "memory");
+  if (hasB) {
+    Acc<KS> delta;
+    pm_mfma<KS>(M, fb, AT, LD, tid, delta);
+    pp_epilogue<F32OUT, KS, FULL, FMT>(M.base, fb, delta, i0, gB, tid);
+  }
+}
+
+template <bool F32OUT, int KS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_fused_pair_multi(JobTable tab) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
+  const int tid = threadIdx.x;
+  const uint32_t pair = xcd_remap(blockIdx.x, gridDim.x);
+  const PJM M = pjm_load(tab, pair);
+  const uint32_t p = pair - M.base.unit_begin;
+  const uint32_t i0 = (p % M.base.bands_n) * kBandCols;
+  const uint32_t gA = (p / M.base.bands_n) * (2 * kWavesPerGroup * kStripRows);
+  const uint32_t gB = gA + kWavesPerGroup * kStripRows;
+  const bool hasB = gB < M.base.rows;
+  const bool full = gB + kWavesPerGroup * kStripRows <= M.base.rows && i0 + kBandCols <= M.base.cols;
+  if (M.base.fmt == 0) {
+    if (full) pair_units_multi<F32OUT, KS, 0, true>(M, AT, i0, gA, gB, hasB, tid);
+    else pair_units_multi<F32OUT, KS, 0, false>(M, AT, i0, gA, gB, hasB, tid);
+  } else {
+    if (full) pair_units_multi<F32OUT, KS, 1, true>(M, AT, i0, gA, gB, hasB, tid);
+    else pair_units_multi<F32OUT, KS, 1, false>(M, AT, i0, gA, gB, hasB, tid);
+  }
+}
+
 template <int FMT, int SMODE>
 hipError_t dequant_dispatch_out(const DequantArgs& a, bool f32out, dim3 grid, hipStream_t s) {
   if (f32out)
@@ -892,11 +832,16 @@ hipError_t launch_dequant(const DequantArgs& a, int fmt, int scale_mode, bool f3
 
 template <int KS>
 hipError_t launch_fused_ks(const JobTable& t, bool f32out, bool multi, dim3 grid, size_t lds, hipStream_t stream) {
-  if (f32out) {
-    if (multi) hipLaunchKernelGGL((k_fused<true, true, KS>), grid, dim3(256), lds, stream, t);
-    else hipLaunchKernelGGL((k_fused_pair<true, KS>), grid, dim3(256), lds, stream, t);
+  if (multi) {
+    // Two or more LoRAs pad to at least two K-steps.
+    if constexpr (KS >= 2) {
+      if (f32out) hipLaunchKernelGGL((k_fused_pair_multi<true, KS>), grid, dim3(256), lds, stream, t);
+      else hipLaunchKernelGGL((k_fused_pair_multi<false, KS>), grid, dim3(256), lds, stream, t);
+    } else {
+      return hipErrorInvalidValue;
+    }
   } else {
-    if (multi) hipLaunchKernelGGL((k_fused<false, true, KS>), grid, dim3(256), lds, stream, t);
+    if (f32out) hipLaunchKernelGGL((k_fused_pair<true, KS>), grid, dim3(256), lds, stream, t);
     else hipLaunchKernelGGL((k_fused_pair<false, KS>), grid, dim3(256), lds, stream, t);
   }
   return hipGetLastError();

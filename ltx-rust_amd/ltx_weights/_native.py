@@ -234,6 +234,7 @@ class Context:
         h = ctypes.c_void_p()
         check(lib().ltxw_ctx_create(device, staging_bytes, n_staging, ctypes.byref(h)), None)
         self.h = h
+        self.device = device
 
     def close(self):
         if self.h:

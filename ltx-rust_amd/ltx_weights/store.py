@@ -11,6 +11,7 @@ import ctypes
 
 import numpy as np
 
+from . import _dlpack
 from . import _native as N
 
 DTYPE_NAMES = ["BOOL", "U8", "I8", "F8_E5M2", "F8_E4M3", "I16", "U16", "F16", "BF16", "I32", "U32",
@@ -176,6 +177,18 @@ class DeviceTensor:
         if self.ptr:
             self.ctx.free(self.ptr)
             self.ptr = None
+
+    # DLPack export: the tensor's HBM, no copy, for any DLPack consumer in the
+    # process that uses the same HIP runtime. The capsule does not own the
+    # memory: keep this DeviceTensor alive (and unfreed) while it is in use.
+    def __dlpack_device__(self):
+        return (_dlpack.KDL_ROCM, self.ctx.device)
+
+    def __dlpack__(self, stream=None):
+        if not self.ptr and self.numel:
+            raise N.InvalidArgument("tensor was freed")
+        self.ctx.synchronize()  # the data is complete before any consumer stream uses it
+        return _dlpack.capsule(self.ptr, self.shape, self.out_dtype == N.OUT_BF16, self.ctx.device, owner=self)
 
 
 class WeightStore:

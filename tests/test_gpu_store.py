@@ -7,6 +7,8 @@ operation order (non-bf16 factors, non-FP8 bases) bit-exact in f32 and bf16;
 bf16 factors on FP8 bases (MFMA path) within 1 bf16 ulp + the Frobenius
 bound of gpu_util.compare_lora_bf16.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -373,3 +375,33 @@ def test_transforms_bit_exact_random(ctx, tmp):
     want = O.read_f32(w8[2:4], O.E4M3FN, O.SCALE_TENSOR, np.array([s_scale], np.float32),
                       [(b, a, O.F32, O.lora_coeff(0.5, None, 3))])
     assert np.array_equal(bits(store.read("n.attn.to_k.weight", ctx)[1]), bits(want))
+
+
+# ---------------------------------------------------------------------------
+# Device hand-off: materialise into a consumer framework's own tensors
+# ---------------------------------------------------------------------------
+def test_dlpack_export_of_materialised_tensor(ctx, tmp):
+    """A materialised tensor exports a DLPack capsule over its own HBM (no
+    copy): ROCm device, bf16, row-major shape and strides, and the data the
+    capsule points at is the materialised result."""
+    from ltx_weights import _dlpack
+    log("dlpack export")
+    case = synth.tensor_case(31, 256, 512, synth.E4M3FN, synth.SCALE_ROW, loras=((64, 1.0),))
+    store = WeightStore.open([tmp([("l.weight", "F8_E4M3", [256, 512], case["w"]),
+                                   ("l.weight_scale", "F32", [256], case["scales"])])])
+    t = store.materialize_bf16(ctx, ["l.weight"])["l.weight"]
+    try:
+        assert t.__dlpack_device__() == (_dlpack.KDL_ROCM, 0)
+        cap = t.__dlpack__()
+        mt = _dlpack.view(cap)
+        dl = mt.dl_tensor
+        assert dl.data == t.ptr and dl.ndim == 2 and dl.byte_offset == 0
+        assert (dl.device.device_type, dl.device.device_id) == (_dlpack.KDL_ROCM, 0)
+        assert (dl.dtype.code, dl.dtype.bits, dl.dtype.lanes) == (_dlpack.KDL_BFLOAT, 16, 1)
+        assert [dl.shape[0], dl.shape[1]] == [256, 512] and [dl.strides[0], dl.strides[1]] == [512, 1]
+        out = np.empty((256, 512), np.uint16)
+        ctx.download(dl.data, out)
+        assert np.array_equal(out, O.read_bf16(case["w"], O.E4M3FN, O.SCALE_ROW, case["scales"]))
+        mt.deleter(ctypes.pointer(mt))  # the consumer's release
+    finally:
+        t.free()
