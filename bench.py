@@ -364,6 +364,8 @@ def main():
                     help="whole-model materialisation reported beside the kernel workload "
                          "(auto: the 22B set beside the default layer workload, none otherwise)")
     ap.add_argument("--e2e-steps", type=int, default=3)
+    ap.add_argument("--exact", action="store_true",
+                    help="LoRA deltas in the reference's operation order (LTXW_DESC_EXACT, bit-identical)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -388,6 +390,10 @@ def main():
     ctx = lw.Context(0)
     stream = ctx.stream()
     insts, allocs, n_inst = build_instances(ctx, cases, hip, stream)
+    if args.exact:
+        for inst in insts:
+            for d in inst:
+                d["flags"] = lw.DESC_EXACT
     log(f"{n_inst} rotating instances")
     ctx.synchronize()
 
@@ -433,7 +439,11 @@ def main():
         out = np.empty((c["rows"], c["cols"]), dtype=np.uint16)
         ctx.download(d["out"], out)
         sel = np.unique(np.linspace(0, c["rows"] - 1, 64).astype(np.int64))
-        if c["loras"]:
+        if c["loras"] and args.exact:
+            stats = {"bit_exact": bool(np.array_equal(U.oracle_bf16(c, row_sel=sel), out[sel]))}
+            if not stats["bit_exact"]:
+                raise AssertionError("exact-mode output differs from the oracle")
+        elif c["loras"]:
             stats = U.compare_lora_bf16(c, out[sel], row_sel=sel)
         else:
             ref = U.oracle_bf16(c, row_sel=sel)
@@ -481,7 +491,8 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded: uniform non-NaN FP8 codes, U[1e-3,1e-1] scales, N(0,0.02^2) bf16 factors)",
-        "config": {"workload": WORKLOAD_TEXT[args.workload], "name": args.workload, "tensors": len(cases),
+        "config": {"workload": WORKLOAD_TEXT[args.workload] + (" (exact mode)" if args.exact else ""),
+                   "name": args.workload + ("-exact" if args.exact else ""), "tensors": len(cases),
                    "params": int(sum(c["rows"] * c["cols"] for c in cases)), "rotating_instances": n_inst},
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBPS, 4),

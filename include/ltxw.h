@@ -103,8 +103,16 @@ typedef struct {
   int32_t scale_mode;      /* ltxw_scale_mode */
   int32_t out_dtype;       /* ltxw_out_dtype */
   int32_t n_loras;         /* 0..LTXW_MAX_LORAS, merged in array order */
+  int32_t flags;           /* LTXW_DESC_* */
   ltxw_lora loras[LTXW_MAX_LORAS];
 } ltxw_tensor_desc;
+
+/* Bit-identical results with LoRA deltas: the reference's own operation
+ * order (per element, per rank: w = fma(coeff * B[o,r], A[r,i], w)) instead
+ * of the MFMA product. Slower (r FMAs per element on the vector units).
+ * Tensors without deltas, and deltas the MFMA path does not take, are
+ * bit-identical either way. */
+#define LTXW_DESC_EXACT 1
 
 typedef struct ltxw_ctx ltxw_ctx;
 

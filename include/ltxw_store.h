@@ -133,6 +133,9 @@ int ltxw_store_delta(const ltxw_store* s, const char* key, int index, int32_t* r
  * the reference does for all (src/store.rs:498-508, :732-735; empty: 1.0).
  * LTXW_MAT_SCALE_FIRST applies the reference's element-0 rule to all. */
 #define LTXW_MAT_SCALE_FIRST 1u
+/* Bit-identical LoRA merges: every key with deltas in the reference's
+ * operation order (LTXW_DESC_EXACT). */
+#define LTXW_MAT_EXACT 2u
 
 /* Materialise tensors into caller-allocated device buffers: outs[k] holds
  * numel(keys[k]) elements of out_dtype (ltxw_out_dtype) in row-major order.

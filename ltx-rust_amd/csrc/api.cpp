@@ -108,6 +108,7 @@ int check_desc(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t* n) {
     return fail(ctx, LTXW_ERR_INVALID_ARG, "invalid output dtype %d", d.out_dtype);
   if (d.n_loras < 0 || d.n_loras > LTXW_MAX_LORAS)
     return fail(ctx, LTXW_ERR_INVALID_ARG, "n_loras %d outside [0, %d]", d.n_loras, LTXW_MAX_LORAS);
+  if (d.flags & ~LTXW_DESC_EXACT) return fail(ctx, LTXW_ERR_INVALID_ARG, "unknown descriptor flags 0x%x", d.flags);
   if (*n == 0) return LTXW_OK;
   if (!d.w || !d.out) return fail(ctx, LTXW_ERR_INVALID_ARG, "null weight or output pointer");
   if (!aligned(d.w, (size_t)esize))
@@ -189,6 +190,21 @@ int run_generic(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t begin, uint64
     g.post_mul = ex->post_mul;
   }
   HIP_TRY(ctx, ltxw::launch_generic(g, d.out_dtype == LTXW_OUT_F32, ctx->compute), "generic kernel launch");
+  return LTXW_OK;
+}
+
+// Reference-order tiled kernel over the whole tensor (LoRA deltas in the
+// reference's order, any factor type, base format, shape and alignment).
+int run_exact(ltxw_ctx* ctx, const ltxw_tensor_desc& d, const ltxw::DescEx* ex) {
+  ltxw::ExactArgs a{};
+  a.job = to_job(d);
+  if (ex) {
+    a.plain_scale = ex->plain_scale;
+    a.has_post = ex->has_post;
+    a.post_mul = ex->post_mul;
+  }
+  a.bands_n = (uint32_t)((d.cols + ltxw::kExactCols - 1) / ltxw::kExactCols);
+  HIP_TRY(ctx, ltxw::launch_exact(a, d.out_dtype == LTXW_OUT_F32, ctx->compute), "exact kernel launch");
   return LTXW_OK;
 }
 
@@ -292,15 +308,14 @@ int ltxw::run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n, const D
     uint64_t cnt = counts[(size_t)k];
     if (cnt == 0) continue;
     int rc = LTXW_OK;
-    if (ex && (ex[k].plain_scale || ex[k].has_post)) {
-      rc = run_generic(ctx, d, 0, cnt, &ex[k]);
-    } else if (d.n_loras == 0 && ltxw::format_bytes(d.fmt) == 1) {
-      rc = run_dequant(ctx, d, cnt);
-    } else if (fused_ok(d)) {
+    const bool extras = ex && (ex[k].plain_scale || ex[k].has_post);
+    if (extras || (d.n_loras > 0 && ((d.flags & LTXW_DESC_EXACT) || !fused_ok(d)))) {
+      rc = run_exact(ctx, d, extras ? &ex[k] : nullptr);
+    } else if (d.n_loras == 0) {
+      rc = ltxw::format_bytes(d.fmt) == 1 ? run_dequant(ctx, d, cnt) : run_generic(ctx, d, 0, cnt);
+    } else {
       ltxw::JobDev j = to_job(d);
       buckets[{d.out_dtype == LTXW_OUT_F32, d.n_loras > 1, job_k(j) / 32}].push_back(j);
-    } else {
-      rc = run_generic(ctx, d, 0, cnt);
     }
     if (rc) return rc;
   }

@@ -73,6 +73,19 @@ struct GenericArgs {
   float post_mul;
 };
 
+// Tiled reference-order kernel (any shape, alignment, base format and factor
+// type): the generic kernel's arithmetic with the factors staged in LDS.
+struct ExactArgs {
+  JobDev job;
+  int32_t plain_scale;  // as GenericArgs
+  int32_t has_post;
+  float post_mul;
+  uint32_t bands_n;     // ceil(cols / kExactCols)
+};
+constexpr int kExactCols = 128;
+constexpr int kExactRows = 64;
+hipError_t launch_exact(const ExactArgs& a, bool f32out, hipStream_t stream);
+
 // Streaming dequant: n_chunks * 16 elements. Pointers 16-byte aligned.
 hipError_t launch_dequant(const DequantArgs& a, int fmt, int scale_mode, bool f32out,
                           hipStream_t stream);

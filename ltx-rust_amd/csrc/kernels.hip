@@ -225,6 +225,125 @@ __global__ __launch_bounds__(256) void k_generic(GenericArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// Tiled reference-order kernel: the arithmetic of k_generic (bit-identical to
+// the reference's f32), with the LoRA factors staged through LDS.
+// Workgroup: 128 columns x 64 rows; thread (cg = tid % 16, rs = tid / 16)
+// owns columns i0 + 8*cg .. +7 of rows g0 + rs + 16*k, k < 4. Per LoRA, the
+// ranks go in chunks of 32: A[r][band] and B[rows][r] widened to f32 into
+// LDS, then every thread runs w = fma(coeff * B[o][r], A[r][i], w) in r order.
+// VALU-bound (r FMAs per element); for adapters whose factors are not bf16,
+// non-FP8 bases, odd shapes, and bit-exact requests.
+// ---------------------------------------------------------------------------
+constexpr int kExactR = 32;
+
+// Factor element e widened to f32, element type fixed at compile time
+// (FDT = kMixedFactors: the LoRA's own, read at run time).
+constexpr int kMixedFactors = 5;
+template <int FDT>
+__device__ __forceinline__ float factor_at(const void* p, int dt, uint64_t e) {
+  if constexpr (FDT == kMixedFactors) return load_factor(p, dt, e);
+  else if constexpr (FDT == 0) return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[e]);
+  else if constexpr (FDT == 1) return reinterpret_cast<const float*>(p)[e];
+  else if constexpr (FDT == 2) return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[e]);
+  else return canon_nan(decode1(reinterpret_cast<const uint8_t*>(p)[e], FDT - 3));
+}
+
+template <bool F32OUT, int FDT>
+__global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
+  __shared__ __attribute__((aligned(16))) float As[kExactR][kExactCols];
+  __shared__ float Bs[kExactRows][kExactR + 1];
+  const JobDev& J = g.job;
+  const int tid = threadIdx.x, cg = tid & 15, rs = tid >> 4;
+  const uint64_t rows = (uint64_t)J.rows, cols = (uint64_t)J.cols;
+  const uint64_t band = blockIdx.x % g.bands_n, grp = blockIdx.x / g.bands_n;
+  const uint64_t i0 = band * kExactCols, g0 = grp * kExactRows;
+  const uint64_t c0 = i0 + 8 * cg;
+  // FP8 rows of 8 whole, aligned elements load as one 8-byte word.
+  const bool vec8 = J.fmt <= 1 && c0 + 8 <= cols && (cols & 7) == 0 && (((uintptr_t)J.w) & 7) == 0;
+  float acc[4][8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint64_t o = g0 + rs + 16 * k;
+    if (o < rows && vec8) {
+      const u32x2 wv = *reinterpret_cast<const u32x2*>(J.w + o * cols + c0);
+      decode4(wv[0], J.fmt, acc[k]);
+      decode4(wv[1], J.fmt, acc[k] + 4);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[k][j] = canon_nan(acc[k][j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint64_t i = c0 + j;
+        acc[k][j] = (o < rows && i < cols) ? load_base(J, o * cols + i) : 0.0f;
+      }
+    }
+    if (o < rows) {
+      const float s = J.scale_mode == 0 ? 1.0f : J.scales[J.scale_mode == 2 ? o : 0];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float v = acc[k][j];
+        if (J.scale_mode != 0) v = g.plain_scale ? s * v : __builtin_fmaf(s, v, 0.0f);
+        if (g.has_post) v = v * g.post_mul;
+        acc[k][j] = v;
+      }
+    }
+  }
+  for (int l = 0; l < J.n_loras && l < kMaxLoras; ++l) {
+    const LoraDev L = J.lora[l];
+    const uint64_t rank = (uint64_t)L.rank;
+    for (uint64_t r0 = 0; r0 < rank; r0 += kExactR) {
+      __syncthreads();  // the previous chunk has been consumed
+      {
+        const uint64_t rr = r0 + (tid >> 3);
+        const int cc = (tid & 7) * 16;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const uint64_t ii = i0 + cc + q;
+          As[tid >> 3][cc + q] = (rr < rank && ii < cols) ? factor_at<FDT>(L.a, L.dtype, rr * cols + ii) : 0.0f;
+        }
+        const uint64_t oo = g0 + (tid >> 2);
+        const int q0 = (tid & 3) * 8;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const uint64_t rq = r0 + q0 + q;
+          Bs[tid >> 2][q0 + q] = (oo < rows && rq < rank) ? factor_at<FDT>(L.b, L.dtype, oo * rank + rq) : 0.0f;
+        }
+      }
+      __syncthreads();
+      const int nr = (int)(rank - r0 < (uint64_t)kExactR ? rank - r0 : (uint64_t)kExactR);
+      // Zero-padded ranks beyond nr add fma(c, 0, w) = w + 0, which is not
+      // the identity on -0; so the loop stops at nr exactly.
+#pragma unroll 4
+      for (int r = 0; r < nr; ++r) {
+        const f32x4 a0 = *reinterpret_cast<const f32x4*>(&As[r][8 * cg]);
+        const f32x4 a1 = *reinterpret_cast<const f32x4*>(&As[r][8 * cg + 4]);
+        const float a[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float c = L.coeff * Bs[rs + 16 * k][r];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[k][j] = __builtin_fmaf(c, a[j], acc[k][j]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint64_t o = g0 + rs + 16 * k;
+    if (o >= rows) continue;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint64_t i = c0 + j;
+      if (i >= cols) continue;
+      float v = acc[k][j];
+      if (J.fmt <= 1) v = canon_nan(v);
+      if (F32OUT) reinterpret_cast<float*>(J.out)[o * cols + i] = v;
+      else reinterpret_cast<uint16_t*>(J.out)[o * cols + i] = bf16_rne(v);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // (b) Fused dequant + LoRA merge.
 //
 // Work unit: one band of 128 output columns [i0, i0+128) by 128 rows; each of
@@ -861,6 +980,33 @@ hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, hipStream_t 
     case 7: return launch_fused_ks<7>(t, f32out, multi, grid, lds, stream);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_exact(const ExactArgs& a, bool f32out, hipStream_t stream) {
+  const uint64_t rows = (uint64_t)a.job.rows;
+  const uint64_t groups = (rows + kExactRows - 1) / kExactRows;
+  const uint64_t blocks = groups * (uint64_t)a.bands_n;
+  if (blocks == 0) return hipSuccess;
+  if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+  dim3 grid((unsigned)blocks);
+  // One compiled factor type when every LoRA of the tensor shares it.
+  int fdt = a.job.n_loras > 0 ? a.job.lora[0].dtype : 0;
+  for (int l = 1; l < a.job.n_loras && l < kMaxLoras; ++l)
+    if (a.job.lora[l].dtype != fdt) fdt = kMixedFactors;
+#define LTXW_EXACT_LAUNCH(F)                                                              \
+  if (f32out) hipLaunchKernelGGL((k_exact<true, F>), grid, dim3(256), 0, stream, a);     \
+  else hipLaunchKernelGGL((k_exact<false, F>), grid, dim3(256), 0, stream, a);
+  switch (fdt) {
+    case 0: LTXW_EXACT_LAUNCH(0) break;
+    case 1: LTXW_EXACT_LAUNCH(1) break;
+    case 2: LTXW_EXACT_LAUNCH(2) break;
+    case 3: LTXW_EXACT_LAUNCH(3) break;
+    case 4: LTXW_EXACT_LAUNCH(4) break;
+    case kMixedFactors: LTXW_EXACT_LAUNCH(kMixedFactors) break;
+    default: return hipErrorInvalidValue;
+  }
+#undef LTXW_EXACT_LAUNCH
+  return hipGetLastError();
 }
 
 hipError_t launch_generic(const GenericArgs& a, bool f32out, hipStream_t stream) {

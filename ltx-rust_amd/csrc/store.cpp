@@ -520,7 +520,7 @@ constexpr uint64_t kMaxRun = 256ull << 20;
 //                 piece order; after a batch's last piece, the compute stream
 //                 waits for the copies and runs the batch's kernels.
 // Host reads finish before return; device work completes in stream order.
-int run_pipeline(ltxw_ctx* ctx, std::vector<Plan>& plans, int out_dtype) {
+int run_pipeline(ltxw_ctx* ctx, std::vector<Plan>& plans, int out_dtype, uint32_t flags) {
   if (plans.empty()) return LTXW_OK;
   hipError_t he;
   if ((he = hipSetDevice(ctx->device)) != hipSuccess)
@@ -687,6 +687,7 @@ int run_pipeline(ltxw_ctx* ctx, std::vector<Plan>& plans, int out_dtype) {
       d.scale_mode = p.scale_mode;
       d.out_dtype = out_dtype;
       d.n_loras = (int32_t)p.deltas.size();
+      d.flags = (flags & LTXW_MAT_EXACT) ? LTXW_DESC_EXACT : 0;
       for (size_t l = 0; l < p.deltas.size(); ++l)
         d.loras[l] = {base + p.off_b[l], base + p.off_a[l], (int32_t)p.deltas[l]->rank, p.deltas[l]->coeff,
                       p.fdt[l], 0};
@@ -718,7 +719,7 @@ int materialize(ltxw_store* s, ltxw_ctx* ctx, const char* const* keys, int64_t n
     return sfail(LTXW_ERR_INVALID_ARG, "invalid key or output array");
   if (out_dtype != LTXW_OUT_BF16 && out_dtype != LTXW_OUT_F32)
     return sfail(LTXW_ERR_INVALID_ARG, "invalid output dtype %d", out_dtype);
-  if (flags & ~LTXW_MAT_SCALE_FIRST) return sfail(LTXW_ERR_INVALID_ARG, "unknown flags 0x%x", flags);
+  if (flags & ~(LTXW_MAT_SCALE_FIRST | LTXW_MAT_EXACT)) return sfail(LTXW_ERR_INVALID_ARG, "unknown flags 0x%x", flags);
   // Resolve and check every key before any work is queued.
   std::vector<Plan> plans;
   plans.reserve((size_t)n_keys);
@@ -728,7 +729,7 @@ int materialize(ltxw_store* s, ltxw_ctx* ctx, const char* const* keys, int64_t n
     if (int rc = make_plan(s, keys[k], flags, out_dtype, outs[k], &p)) return rc;
     if (p.numel) plans.push_back(std::move(p));
   }
-  return run_pipeline(ctx, plans, out_dtype);
+  return run_pipeline(ctx, plans, out_dtype, flags);
 }
 
 }  // namespace

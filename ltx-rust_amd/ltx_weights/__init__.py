@@ -5,6 +5,7 @@ include/ltxw.h and include/ltxw_store.h (the library is libltxw.so, built
 in-tree for gfx950).
 """
 from ._native import (  # noqa: F401
+    DESC_EXACT,
     FACTOR_BF16,
     FACTOR_E4M3FN,
     FACTOR_E5M2,

@@ -108,8 +108,12 @@ class TensorDesc(ctypes.Structure):
         ("scale_mode", ctypes.c_int32),
         ("out_dtype", ctypes.c_int32),
         ("n_loras", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
         ("loras", Lora * MAX_LORAS),
     ]
+
+
+DESC_EXACT = 1
 
 
 class KeyRule(ctypes.Structure):
@@ -299,6 +303,7 @@ class Context:
             t.rows, t.cols = d["rows"], d["cols"]
             t.fmt, t.scale_mode = d.get("fmt", FMT_E4M3FN), d.get("scale_mode", SCALE_NONE)
             t.out_dtype = d.get("out_dtype", OUT_BF16)
+            t.flags = d.get("flags", 0)
             loras = d.get("loras", [])
             t.n_loras = len(loras)
             for l, x in enumerate(loras[:MAX_LORAS]):

@@ -17,6 +17,7 @@ from . import _native as N
 DTYPE_NAMES = ["BOOL", "U8", "I8", "F8_E5M2", "F8_E4M3", "I16", "U16", "F16", "BF16", "I32", "U32",
                "F32", "F64", "I64", "U64", "F8_E8M0", "F4", "F6_E2M3", "F6_E3M2", "C64"]
 MAT_SCALE_FIRST = 1
+MAT_EXACT = 2
 _MAX_DIMS = 16
 
 

@@ -261,3 +261,60 @@ def test_upload_download_round_trip(ctx):
         assert np.array_equal(x, y)
     finally:
         ctx.free(p)
+
+
+# ---------------------------------------------------------------------------
+# Exact mode (LTXW_DESC_EXACT): the reference's own operation order, bit for bit
+# ---------------------------------------------------------------------------
+def run_grouped(ctx, cases, out_dtype=lw.OUT_BF16, flags=0):
+    devs = [U.Dev(ctx, c, out_dtype) for c in cases]
+    try:
+        descs = [{"w": d.w, "out": d.out, "scales": d.s, "rows": c["rows"], "cols": c["cols"], "fmt": c["fmt"],
+                  "scale_mode": c["scale_mode"], "out_dtype": out_dtype, "loras": d.loras, "flags": flags}
+                 for d, c in zip(devs, cases)]
+        ctx.grouped(descs)
+        return [d.result() for d in devs]
+    finally:
+        for d in devs:
+            d.free()
+
+
+@pytest.mark.parametrize("rows,cols,ranks,fmt,scale_mode", [
+    (512, 1024, ((64, 1.0),), synth.E4M3FN, synth.SCALE_ROW),
+    (300, 520, ((32, 1.0), (128, 0.5)), synth.E5M2, synth.SCALE_ROW),
+    (129, 136, ((8, 0.75),), synth.E4M3FN, synth.SCALE_TENSOR),
+    (64, 8, ((3, 1.25), (5, -0.5), (2, 2.0)), synth.E5M2, synth.SCALE_NONE),
+])
+def test_exact_mode_bit_exact(ctx, rows, cols, ranks, fmt, scale_mode):
+    """With LTXW_DESC_EXACT every delta runs in the reference's order: bf16 and
+    f32 outputs equal the oracle bit for bit, shapes the MFMA path would take
+    included."""
+    log("case: exact", rows, cols, ranks, fmt, scale_mode)
+    case = synth.tensor_case(rows * 7 + cols, rows, cols, fmt, scale_mode, loras=ranks)
+    for out_dtype in (lw.OUT_BF16, lw.OUT_F32):
+        got, = run_grouped(ctx, [case], out_dtype, flags=lw.DESC_EXACT)
+        ref = U.oracle_bf16(case) if out_dtype == lw.OUT_BF16 else U.oracle_f32(case)
+        view = np.uint16 if out_dtype == lw.OUT_BF16 else np.uint32
+        assert np.array_equal(got.view(view), ref.view(view))
+
+
+def test_exact_mode_nan_inf_codes(ctx):
+    log("case: exact nan/inf")
+    for fmt in (lw.FMT_E4M3FN, lw.FMT_E5M2):
+        case = all_codes_case(fmt, lw.SCALE_ROW, rows=64, cols=256)
+        rng = np.random.default_rng(5)
+        b, a = synth.lora_factors(rng, 64, 256, 32)
+        case["loras"] = [(b, a, 32, 1.0)]
+        got, = run_grouped(ctx, [case], lw.OUT_BF16, flags=lw.DESC_EXACT)
+        assert np.array_equal(got, U.oracle_bf16(case))
+
+
+def test_exact_and_fused_agree_within_tolerance(ctx):
+    """The MFMA path stays within the stated tolerance of the exact path's
+    (= the reference's) result on the same launch."""
+    log("case: exact vs fused")
+    case = synth.tensor_case(991, 512, 512, synth.E4M3FN, synth.SCALE_ROW, loras=((64, 1.0),))
+    exact, = run_grouped(ctx, [case], flags=lw.DESC_EXACT)
+    fused, = run_grouped(ctx, [case], flags=0)
+    assert np.array_equal(exact, U.oracle_bf16(case))
+    assert int(np.abs(U.bf16_ordered(exact) - U.bf16_ordered(fused)).max()) <= 1

@@ -17,7 +17,7 @@ import ltx_weights as lw
 import oracle_lib as O
 import st_io
 from ltx_weights import synth
-from ltx_weights.store import MAT_SCALE_FIRST, KeyMap, LoraFile, WeightStore
+from ltx_weights.store import MAT_EXACT, MAT_SCALE_FIRST, KeyMap, LoraFile, WeightStore
 
 pytestmark = pytest.mark.gpu
 
@@ -405,3 +405,57 @@ def test_dlpack_export_of_materialised_tensor(ctx, tmp):
         mt.deleter(ctypes.pointer(mt))  # the consumer's release
     finally:
         t.free()
+
+
+def test_exact_materialise_of_synthetic_block(ctx, tmp_path):
+    """LTXW_MAT_EXACT: a DiT block (two stacked bf16 LoRAs, mixed formats)
+    bit-identical to the reference order on sampled rows."""
+    log("exact materialise: writing files")
+    m, l1, l2 = (tmp_path / n for n in ("m.safetensors", "l1.safetensors", "l2.safetensors"))
+    synth.write_model(m, 705, 1, variant=1, threads=8)
+    synth.write_lora(l1, 706, 1, 32, variant=1, threads=8)
+    synth.write_lora(l2, 707, 1, 128, variant=1, threads=8)
+    store = WeightStore.open([m], KeyMap.transformer())
+    store.merge_lora(LoraFile.open(l1), 1.0)
+    store.merge_lora(LoraFile.open(l2), 0.5)
+    layout = synth.model_layout(1, 1)
+    keys = [k for k, *_ in layout]
+    outs = {}
+    try:
+        for k, (key, fmt, sm, r, c) in enumerate(layout):
+            outs[key] = ctx.alloc(2 * r * c)
+        store.materialize(ctx, keys, [outs[k] for k in keys], lw.OUT_BF16, MAT_EXACT)
+        for key, fmt, sm, r, c in layout[7:]:
+            rows = np.array([0, r // 2, r - 1])
+            w, sc = synth.model_rows(705, key, fmt, sm, rows, c, r)
+            b1, a1 = synth.lora_factors_rows(706, key, 32, rows, r, c)
+            b2, a2 = synth.lora_factors_rows(707, key, 128, rows, r, c)
+            full = np.empty((r, c), np.uint16)
+            ctx.download(outs[key], full)
+            ref = O.read_bf16(w, U.FMT_TO_ORC[fmt], sm, sc[rows] if sm == synth.SCALE_ROW else sc,
+                              [(b1, a1, O.BF16, O.lora_coeff(1.0, None, 32)),
+                               (b2, a2, O.BF16, O.lora_coeff(0.5, None, 128))])
+            assert np.array_equal(full[rows], ref), key
+    finally:
+        for p in outs.values():
+            ctx.free(p)
+
+
+def test_mixed_factor_types_on_one_tensor(ctx, tmp):
+    """A bf16 adapter and an f32 adapter stacked on one key: reference order,
+    bit-exact (the exact kernel reads each LoRA's own element type)."""
+    log("mixed factor types")
+    rng = np.random.default_rng(23)
+    rows, cols = 96, 136
+    w = synth.E4M3FN_CODES[rng.integers(0, 254, (rows, cols))]
+    sc = rng.uniform(1e-3, 1e-1, rows).astype(np.float32)
+    store = WeightStore.open([tmp([("x.weight", "F8_E4M3", [rows, cols], w), ("x.weight_scale", "F32", [rows], sc)])])
+    a1, b1 = factor_bits(rng, "BF16", (16, cols), 0.05), factor_bits(rng, "BF16", (rows, 16), 0.05)
+    a2, b2 = factor_bits(rng, "F32", (8, cols), 0.05), factor_bits(rng, "F32", (rows, 8), 0.05)
+    store.merge_lora(LoraFile.open(tmp([("x.lora_A.weight", "BF16", [16, cols], a1),
+                                        ("x.lora_B.weight", "BF16", [rows, 16], b1)])), 1.0)
+    store.merge_lora(LoraFile.open(tmp([("x.lora_A.weight", "F32", [8, cols], a2),
+                                        ("x.lora_B.weight", "F32", [rows, 8], b2)])), 0.5)
+    want = O.read_f32(w, O.E4M3FN, O.SCALE_ROW, sc, [(b1, a1, O.BF16, O.lora_coeff(1.0, None, 16)),
+                                                     (b2, a2, O.F32, O.lora_coeff(0.5, None, 8))])
+    assert np.array_equal(bits(store.read("x.weight", ctx)[1]), bits(want))
