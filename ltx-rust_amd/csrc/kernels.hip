@@ -296,10 +296,33 @@ __global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
       {
         const uint64_t rr = r0 + (tid >> 3);
         const int cc = (tid & 7) * 16;
+        // 16 consecutive A elements: two (bf16) or four (f32) 16-byte loads
+        // when whole and aligned.
+        const bool a_vec = (FDT == 0 || FDT == 1) && rr < rank && i0 + cc + 16 <= cols && (cols & 7) == 0 &&
+                           (((uintptr_t)L.a) & 15) == 0;
+        if (a_vec) {
+          if constexpr (FDT == 0) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(L.a) + rr * cols + i0 + cc);
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const uint64_t ii = i0 + cc + q;
-          As[tid >> 3][cc + q] = (rr < rank && ii < cols) ? factor_at<FDT>(L.a, L.dtype, rr * cols + ii) : 0.0f;
+            for (int h = 0; h < 2; ++h) {
+              const u32x4 v = src[h];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                As[tid >> 3][cc + 8 * h + 2 * q] = __builtin_bit_cast(float, v[q] << 16);
+                As[tid >> 3][cc + 8 * h + 2 * q + 1] = __builtin_bit_cast(float, v[q] & 0xFFFF0000u);
+              }
+            }
+          } else if constexpr (FDT == 1) {
+            const f32x4* src = reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(L.a) + rr * cols + i0 + cc);
+#pragma unroll
+            for (int h = 0; h < 4; ++h) *reinterpret_cast<f32x4*>(&As[tid >> 3][cc + 4 * h]) = src[h];
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < 16; ++q) {
+            const uint64_t ii = i0 + cc + q;
+            As[tid >> 3][cc + q] = (rr < rank && ii < cols) ? factor_at<FDT>(L.a, L.dtype, rr * cols + ii) : 0.0f;
+          }
         }
         const uint64_t oo = g0 + (tid >> 2);
         const int q0 = (tid & 3) * 8;
@@ -327,18 +350,35 @@ __global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
       }
     }
   }
+  // Whole, aligned groups of 8 columns go out as 16-byte stores.
+  const bool o_vec = c0 + 8 <= cols && (cols & 7) == 0 && (((uintptr_t)J.out) & 15) == 0;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const uint64_t o = g0 + rs + 16 * k;
     if (o >= rows) continue;
+    if (J.fmt <= 1) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[k][j] = canon_nan(acc[k][j]);
+    }
+    if (o_vec) {
+      if (F32OUT) {
+        f32x4* dst = reinterpret_cast<f32x4*>(reinterpret_cast<float*>(J.out) + o * cols + c0);
+        dst[0] = (f32x4){acc[k][0], acc[k][1], acc[k][2], acc[k][3]};
+        dst[1] = (f32x4){acc[k][4], acc[k][5], acc[k][6], acc[k][7]};
+      } else {
+        u32x4 v;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = (uint32_t)bf16_rne(acc[k][2 * q]) | ((uint32_t)bf16_rne(acc[k][2 * q + 1]) << 16);
+        *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(J.out) + o * cols + c0) = v;
+      }
+      continue;
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint64_t i = c0 + j;
       if (i >= cols) continue;
-      float v = acc[k][j];
-      if (J.fmt <= 1) v = canon_nan(v);
-      if (F32OUT) reinterpret_cast<float*>(J.out)[o * cols + i] = v;
-      else reinterpret_cast<uint16_t*>(J.out)[o * cols + i] = bf16_rne(v);
+      if (F32OUT) reinterpret_cast<float*>(J.out)[o * cols + i] = acc[k][j];
+      else reinterpret_cast<uint16_t*>(J.out)[o * cols + i] = bf16_rne(acc[k][j]);
     }
   }
 }
