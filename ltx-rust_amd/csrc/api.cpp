@@ -11,6 +11,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <map>
 #include <mutex>
 #include <thread>
@@ -173,9 +174,39 @@ bool fused_ok(const ltxw_tensor_desc& d) {
     if (d.loras[l].dtype != LTXW_FACTOR_BF16) return false;
     if (r % 8 != 0 || !aligned(d.loras[l].a, 16) || !aligned(d.loras[l].b, 16)) return false;
     if (2 * r * (uint64_t)d.rows > lim || 2 * r * (uint64_t)d.cols > lim) return false;
+    // Several LoRAs share one accumulator, rescaled by c_l / c_{l+1} between
+    // them: keep those ratios and the rescaled partial sums far from f32
+    // overflow and underflow.
+    const float c = std::fabs(d.loras[l].coeff);
+    if (d.n_loras > 1 && !(c >= 0x1p-24f && c <= 0x1p24f)) return false;
     k += ltxw::pad_rank(d.loras[l].rank);
   }
   return k <= ltxw::kRankMax;
+}
+
+// Fills the fused kernels' per-K-step table and coefficient fields of a job
+// that fused_ok accepted (JobDev::qmask, cmul, coeff_out, step).
+void plan_fused(ltxw::JobDev& j) {
+  int t = 0;
+  for (int l = 0; l < j.n_loras; ++l) {
+    const ltxw::LoraDev& L = j.lora[l];
+    const int nks = ltxw::pad_rank(L.rank) / 32;
+    for (int kt = 0; kt < nks && t < ltxw::kMaxSteps; ++kt, ++t) {
+      ltxw::StepDev& s = j.step[t];
+      s.a = L.a + (size_t)32 * kt * (size_t)j.cols;
+      s.b = L.b + 32 * kt;
+      s.rank = (uint32_t)L.rank;
+      s.klim = (uint32_t)(L.rank - 32 * kt);
+      s.q = 1.0f;
+      s.pad = 0;
+    }
+    if (l + 1 < j.n_loras && t >= 1) {
+      j.step[t - 1].q = L.coeff / j.lora[l + 1].coeff;
+      if (j.step[t - 1].q != 1.0f) j.qmask |= 1u << (t - 1);
+    }
+  }
+  j.coeff_out = j.n_loras > 0 ? j.lora[j.n_loras - 1].coeff : 1.0f;
+  j.cmul = j.coeff_out != 1.0f ? 1u : 0u;
 }
 
 int run_generic(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t begin, uint64_t count,
@@ -260,6 +291,7 @@ int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool 
   const int64_t group_rows = ltxw::kPairRows;
   int64_t units = 0;
   for (auto& j : jobs) {
+    plan_fused(j);
     j.unit_begin = units;
     units += (int64_t)j.bands_n * ((j.rows + group_rows - 1) / group_rows);
   }

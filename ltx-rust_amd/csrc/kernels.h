@@ -27,6 +27,19 @@ struct LoraDev {
   int32_t pad;
 };
 
+// One K-step (32 ranks) of the several-LoRA fused kernel, prepared on the
+// host: the LoRAs of a tensor sit side by side along K, each padded to 32,
+// and LoRA l owns the steps [kst_l, kst_l + pad_rank(rank_l) / 32).
+struct StepDev {
+  const uint16_t* a;  // A of the step's LoRA + 32 kt rows (row stride cols)
+  const uint16_t* b;  // B of the step's LoRA + 32 kt columns (row stride rank)
+  uint32_t rank;      // the LoRA's rank
+  uint32_t klim;      // ranks of the step that exist: rank - 32 kt (>= 32: all)
+  float q;            // factor applied to the accumulator after the step
+  uint32_t pad;
+};
+constexpr int kMaxSteps = kRankMax / 32;
+
 // One tensor of a fused launch, as the kernel reads it.
 struct JobDev {
   const uint8_t* w;
@@ -40,6 +53,16 @@ struct JobDev {
   int32_t bands_n;     // column bands (ceil(cols / kBandCols))
   int64_t unit_begin;  // first flat work unit of this job in the launch
   LoraDev lora[kMaxLoras];
+  // Fused kernels only (plan_fused). The accumulated product is multiplied by
+  // coeff_out at the end when cmul is set. With several LoRAs, the step that
+  // ends LoRA l (another one following) multiplies the accumulator by
+  // q = c_l / c_{l+1}, so that it ends as (sum_l c_l B_l A_l) / c_last and one
+  // register set holds the whole delta; qmask has bit t set for such steps.
+  uint32_t qmask;
+  uint32_t cmul;
+  float coeff_out;
+  uint32_t pad;
+  StepDev step[kMaxSteps];
 };
 
 struct JobTable {
@@ -95,7 +118,8 @@ hipError_t launch_dequant(const DequantArgs& a, int fmt, int scale_mode, bool f3
 // total padded rank <= kRankMax, the same K-steps for every job
 // (lds_ld == 8 + 32 * K-steps). One workgroup per pair of vertically
 // adjacent 128-row units (kPairRows rows); unit_begin and total_units count
-// pairs. `multi`: several LoRAs per tensor.
+// pairs. `multi`: several LoRAs per tensor. Every job's qmask, cmul,
+// coeff_out and step[] are filled (plan_fused in api.cpp).
 hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, hipStream_t stream);
 
 // Rows of one workgroup of the single-LoRA kernel.

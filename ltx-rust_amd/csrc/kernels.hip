@@ -427,38 +427,6 @@ __device__ __forceinline__ void load_job(const JobTable& t, uint64_t unit, JobDe
   __builtin_memcpy(&J, raw, sizeof(JobDev));
 }
 
-// K-steps (32 ranks each) of all of a tensor's LoRAs, side by side: LoRA l
-// owns K-steps [kst_l, kst_l + pad_rank(rank_l) / 32). For K-step t of LoRA l
-// (local step kt = t - kst_l), thread tid stages ranks 32*kt + 2*(tid % 16)
-// and +1 of A for the 8 columns i0 + 8*(tid / 16) .. +7 into
-// AT[slot][32*t + ..] with slot = (i % 8) * 16 + i / 8 for local column i.
-struct LoraSteps {
-  int kst[kMaxLoras];   // first K-step of each LoRA
-  int nks[kMaxLoras];   // K-steps of each LoRA
-  int total;            // sum of nks
-};
-
-// Owner LoRA of K-step t, the step's index within that LoRA, and whether it
-// is the LoRA's last step (static loop: no run-time indexing of arrays).
-struct StepInfo {
-  int l;
-  int kt;
-  bool last;
-};
-
-__device__ __forceinline__ StepInfo step_info(const LoraSteps& S, int t) {
-  StepInfo r{0, t, false};
-#pragma unroll
-  for (int q = 0; q < kMaxLoras; ++q) {
-    if (S.nks[q] > 0 && t >= S.kst[q] && t < S.kst[q] + S.nks[q]) {
-      r.l = q;
-      r.kt = t - S.kst[q];
-      r.last = t == S.kst[q] + S.nks[q] - 1;
-    }
-  }
-  return r;
-}
-
 // Loads and stores at a 32-bit byte offset from a wave-uniform base pointer,
 // so the compiler can use the SGPR-base + VGPR-offset addressing mode (one
 // VGPR of address per lane, no 64-bit address arithmetic). The host routes
@@ -502,6 +470,7 @@ struct PJ {
   const uint16_t* b;
   uint32_t rows, cols, rank, bands_n, scale_mode, fmt;
   float coeff;
+  uint32_t cmul;  // coeff applies (coeff != 1)
   uint32_t unit_begin;
 };
 
@@ -520,7 +489,8 @@ __device__ __forceinline__ PJ pj_load(const JobTable& t, uint64_t unit) {
   p.bands_n = uni((uint32_t)J.bands_n);
   p.scale_mode = uni((uint32_t)J.scale_mode);
   p.fmt = uni((uint32_t)J.fmt);
-  p.coeff = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.lora[0].coeff)));
+  p.coeff = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.coeff_out)));
+  p.cmul = uni(J.cmul);
   p.unit_begin = uni((uint32_t)J.unit_begin);
   return p;
 }
@@ -536,6 +506,9 @@ struct Stage {
   u32x4 lo[KS], hi[KS];
 };
 
+// A^T staging: for K-step t, thread tid loads ranks 32 t + 2 (tid % 16) and
+// +1 of A for the 8 columns i0 + 8 (tid / 16) .. +7 and stores them into
+// AT[slot][32 t + ..] with slot = (i % 8) * 16 + i / 8 for local column i.
 template <int KS>
 __device__ __forceinline__ void pp_issue_a(const PJ& J, uint32_t i0, int tid, Stage<KS>& st) {
   const int sq = tid & 15;
@@ -650,7 +623,9 @@ __device__ __forceinline__ void pp_epilogue(const PJ& J, const Frag<KS>& f, Acc<
   const float c = J.coeff;
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb) {
-    if (c != 1.0f) {
+    // A flag from the job, not a test of c: the compiler would turn
+    // `if (c != 1) v *= c` into an unconditional multiply.
+    if (J.cmul) {
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb) a.v[mb][nb] *= c;
     }
@@ -765,23 +740,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 3
 
 // ---------------------------------------------------------------------------
 // Several LoRAs per tensor, two units per workgroup. The LoRAs sit side by
-// side along K (each padded to 32); a LoRA's product is folded into the
-// running delta with its coefficient at the LoRA's last K-step:
-//   delta = c_0 (B_0 A_0) [+ c_1 (B_1 A_1) ...],  y = fma(scale, decode(w), delta).
+// side along K (each padded to 32) and the host describes every K-step
+// (StepDev: the step's A rows, B columns, rank and present ranks). One
+// accumulator set carries the whole delta: at the last step of LoRA l, with
+// LoRA l+1 following, the accumulator is multiplied by q = c_l / c_{l+1}, and
+// the epilogue multiplies by the last coefficient:
+//   delta = c_last (... ((B_0 A_0) q_0 + B_1 A_1) q_1 ...) = sum_l c_l B_l A_l
+// up to a few f32 roundings (the host routes coefficients whose ratios could
+// overflow or underflow to the reference-order kernel).
 // ---------------------------------------------------------------------------
+template <int KS>
 struct PJM {
-  PJ base;  // coeff = 1: the delta already carries the coefficients
-  const uint16_t* a[kMaxLoras];
-  const uint16_t* b[kMaxLoras];
-  uint32_t rank[kMaxLoras];
-  float coeff[kMaxLoras];
-  LoraSteps ls;
+  PJ base;  // coeff / cmul: the last LoRA's coefficient
+  const uint16_t* a[KS];
+  const uint16_t* b[KS];
+  uint32_t rank[KS];
+  uint32_t klim[KS];
+  float q[KS];
+  uint32_t qmask;
 };
 
-__device__ __forceinline__ PJM pjm_load(const JobTable& t, uint64_t unit) {
+template <int KS>
+__device__ __forceinline__ PJM<KS> pjm_load(const JobTable& t, uint64_t unit) {
   JobDev J;
   load_job(t, unit, J);
-  PJM m;
+  PJM<KS> m;
   m.base.w = uni_ptr(J.w);
   m.base.out = uni_ptr(J.out);
   m.base.scales = uni_ptr(J.scales);
@@ -793,64 +776,50 @@ __device__ __forceinline__ PJM pjm_load(const JobTable& t, uint64_t unit) {
   m.base.bands_n = uni((uint32_t)J.bands_n);
   m.base.scale_mode = uni((uint32_t)J.scale_mode);
   m.base.fmt = uni((uint32_t)J.fmt);
-  m.base.coeff = 1.0f;
+  m.base.coeff = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.coeff_out)));
+  m.base.cmul = uni(J.cmul);
   m.base.unit_begin = uni((uint32_t)J.unit_begin);
-  const int nl = (int)uni((uint32_t)J.n_loras);
-  int k0 = 0;
 #pragma unroll
-  for (int l = 0; l < kMaxLoras; ++l) {
-    m.a[l] = uni_ptr(J.lora[l].a);
-    m.b[l] = uni_ptr(J.lora[l].b);
-    m.rank[l] = uni((uint32_t)J.lora[l].rank);
-    m.coeff[l] = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.lora[l].coeff)));
-    m.ls.kst[l] = k0;
-    m.ls.nks[l] = l < nl ? pad_rank((int)m.rank[l]) / 32 : 0;
-    k0 += m.ls.nks[l];
+  for (int s = 0; s < KS; ++s) {
+    m.a[s] = uni_ptr(J.step[s].a);
+    m.b[s] = uni_ptr(J.step[s].b);
+    m.rank[s] = uni(J.step[s].rank);
+    m.klim[s] = uni(J.step[s].klim);
+    m.q[s] = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.step[s].q)));
   }
-  m.ls.total = k0;
+  m.qmask = uni(J.qmask);
   return m;
 }
 
 template <int KS>
-__device__ __forceinline__ void pm_issue_a(const PJM& M, uint32_t i0, int tid, Stage<KS>& st) {
+__device__ __forceinline__ void pm_issue_a(const PJM<KS>& M, uint32_t i0, int tid, Stage<KS>& st) {
   const int sq = tid & 15;
   const uint32_t cols = M.base.cols;
   const uint32_t scol = i0 + 8 * (tid >> 4);
   const bool scol_ok = scol < cols;
+  const uint32_t k = 2 * sq;
 #pragma unroll
   for (int t = 0; t < KS; ++t) {
-    const StepInfo si = step_info(M.ls, t);
-    const uint32_t k = 32 * si.kt + 2 * sq;
     st.lo[t] = (u32x4){0u, 0u, 0u, 0u};
     st.hi[t] = st.lo[t];
-#pragma unroll
-    for (int q = 0; q < kMaxLoras; ++q) {
-      if (si.l != q) continue;  // uniform; keeps the arrays indexed statically
-      if (scol_ok && k < M.rank[q]) st.lo[t] = ld_at<u32x4>(M.a[q], 2 * (k * cols + scol));
-      if (scol_ok && k + 1 < M.rank[q]) st.hi[t] = ld_at<u32x4>(M.a[q], 2 * ((k + 1) * cols + scol));
-    }
+    if (scol_ok && k < M.klim[t]) st.lo[t] = ld_at<u32x4>(M.a[t], 2 * (k * cols + scol));
+    if (scol_ok && k + 1 < M.klim[t]) st.hi[t] = ld_at<u32x4>(M.a[t], 2 * ((k + 1) * cols + scol));
   }
 }
 
 template <int KS, bool FULL>
-__device__ __forceinline__ void pm_issue_f(const PJM& M, uint32_t g0, int tid, Frag<KS>& f) {
+__device__ __forceinline__ void pm_issue_f(const PJM<KS>& M, uint32_t g0, int tid, Frag<KS>& f) {
   const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
   const uint32_t rows = M.base.rows;
   const uint32_t r0 = g0 + kStripRows * wave;
+  const uint32_t kk = 8 * lg;
 #pragma unroll
   for (int t = 0; t < KS; ++t) {
-    const StepInfo si = step_info(M.ls, t);
-    const uint32_t kk = 32 * si.kt + 8 * lg;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) f.bf[t][mb] = (bf16x8){};
-#pragma unroll
-    for (int q = 0; q < kMaxLoras; ++q) {
-      if (si.l != q) continue;
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        const uint32_t ob = r0 + 16 * mb + ln;
-        if (kk < M.rank[q] && (FULL || ob < rows)) f.bf[t][mb] = ld_at<bf16x8>(M.b[q], 2 * (ob * M.rank[q] + kk));
-      }
+    for (int mb = 0; mb < 2; ++mb) {
+      const uint32_t ob = r0 + 16 * mb + ln;
+      f.bf[t][mb] = (bf16x8){};
+      if (kk < M.klim[t] && (FULL || ob < rows)) f.bf[t][mb] = ld_at<bf16x8>(M.b[t], 2 * (ob * M.rank[t] + kk));
     }
   }
   const uint32_t rl = r0 + 4 * lg;
@@ -876,46 +845,34 @@ __device__ __forceinline__ void pm_issue_f(const PJM& M, uint32_t g0, int tid, F
 }
 
 template <int KS>
-__device__ __forceinline__ void pm_mfma(const PJM& M, const Frag<KS>& f, const uint16_t* AT, int ld, int tid,
-                                        Acc<KS>& delta) {
+__device__ __forceinline__ void pm_mfma(const PJM<KS>& M, const Frag<KS>& f, const uint16_t* AT, int ld, int tid,
+                                        Acc<KS>& a) {
   const int lane = tid & 63, ln = lane & 15, lg = lane >> 4;
-  f32x4 acc[2][8];
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int nb = 0; nb < 8; ++nb) a.v[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int t = 0; t < KS; ++t) {
     const int kk = 32 * t + 8 * lg;
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) {
       const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + kk]);
-      acc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][0], at, acc[0][nb], 0, 0, 0);
-      acc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][1], at, acc[1][nb], 0, 0, 0);
+      a.v[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][0], at, a.v[0][nb], 0, 0, 0);
+      a.v[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][1], at, a.v[1][nb], 0, 0, 0);
     }
-    const StepInfo si = step_info(M.ls, t);
-    if (si.last) {
-      float cl = M.coeff[0];
-#pragma unroll
-      for (int q = 1; q < kMaxLoras; ++q)
-        if (si.l == q) cl = M.coeff[q];
-      const bool first = si.l == 0;
+    if (t + 1 < KS && (M.qmask & (1u << t))) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) {
-#pragma unroll
-          for (int v = 0; v < 4; ++v)
-            delta.v[mb][nb][v] = first ? cl * acc[mb][nb][v] : __builtin_fmaf(cl, acc[mb][nb][v], delta.v[mb][nb][v]);
-          acc[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
-        }
+        for (int nb = 0; nb < 8; ++nb) a.v[mb][nb] *= M.q[t];
     }
   }
 }
 
 template <bool F32OUT, int KS, int FMT, bool FULL>
-__device__ __forceinline__ void pair_units_multi(const PJM& M, uint16_t* AT, uint32_t i0, uint32_t gA, uint32_t gB,
-                                                 bool hasB, int tid) {
+__device__ __forceinline__ void pair_units_multi(const PJM<KS>& M, uint16_t* AT, uint32_t i0, uint32_t gA,
+                                                 uint32_t gB, bool hasB, int tid) {
   constexpr int LD = 32 * KS + 8;
   Stage<KS> st;
   pm_issue_a<KS>(M, i0, tid, st);
@@ -926,16 +883,16 @@ __device__ __forceinline__ void pair_units_multi(const PJM& M, uint16_t* AT, uin
   pp_stage<KS>(st, AT, LD, tid);
   __syncthreads();
   {
-    Acc<KS> delta;
-    pm_mfma<KS>(M, fa, AT, LD, tid, delta);
+    Acc<KS> acc;
+    pm_mfma<KS>(M, fa, AT, LD, tid, acc);
     pm_issue_f<KS, FULL>(M, hasB ? gB : gA, tid, fb);
-    pp_epilogue<F32OUT, KS, FULL, FMT>(M.base, fa, delta, i0, gA, tid);
+    pp_epilogue<F32OUT, KS, FULL, FMT>(M.base, fa, acc, i0, gA, tid);
   }
   asm volatile("" ::: "memory");
   if (hasB) {
-    Acc<KS> delta;
-    pm_mfma<KS>(M, fb, AT, LD, tid, delta);
-    pp_epilogue<F32OUT, KS, FULL, FMT>(M.base, fb, delta, i0, gB, tid);
+    Acc<KS> acc;
+    pm_mfma<KS>(M, fb, AT, LD, tid, acc);
+    pp_epilogue<F32OUT, KS, FULL, FMT>(M.base, fb, acc, i0, gB, tid);
   }
 }
 
@@ -944,7 +901,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
   const int tid = threadIdx.x;
   const uint32_t pair = xcd_remap(blockIdx.x, gridDim.x);
-  const PJM M = pjm_load(tab, pair);
+  const PJM<KS> M = pjm_load<KS>(tab, pair);
   const uint32_t p = pair - M.base.unit_begin;
   const uint32_t i0 = (p % M.base.bands_n) * kBandCols;
   const uint32_t gA = (p / M.base.bands_n) * (2 * kWavesPerGroup * kStripRows);
