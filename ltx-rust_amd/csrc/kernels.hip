@@ -472,6 +472,7 @@ struct PJ {
   float coeff;
   uint32_t cmul;  // coeff applies (coeff != 1)
   uint32_t unit_begin;
+  float tscale;   // the per-tensor scale (scale_mode 1), else 1
 };
 
 __device__ __forceinline__ PJ pj_load(const JobTable& t, uint64_t unit) {
@@ -489,6 +490,9 @@ __device__ __forceinline__ PJ pj_load(const JobTable& t, uint64_t unit) {
   p.bands_n = uni((uint32_t)J.bands_n);
   p.scale_mode = uni((uint32_t)J.scale_mode);
   p.fmt = uni((uint32_t)J.fmt);
+  // One uniform load at the start: no per-lane load in the scale branch of
+  // the factor issue (a vector load on one path only costs waits on both).
+  p.tscale = p.scale_mode == 1 ? *G(uni_ptr(J.scales)) : 1.0f;
   p.coeff = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.coeff_out)));
   p.cmul = uni(J.cmul);
   p.unit_begin = uni((uint32_t)J.unit_begin);
@@ -554,9 +558,8 @@ __device__ __forceinline__ void pp_issue_f(const PJ& J, uint32_t i0, uint32_t g0
       }
     }
   } else {
-    const float t = J.scale_mode == 1 ? ld_at<float>(J.scales, 0) : 1.0f;
 #pragma unroll
-    for (int g = 0; g < 8; ++g) f.sc[g] = t;
+    for (int g = 0; g < 8; ++g) f.sc[g] = J.tscale;
   }
 }
 
@@ -776,6 +779,7 @@ __device__ __forceinline__ PJM<KS> pjm_load(const JobTable& t, uint64_t unit) {
   m.base.bands_n = uni((uint32_t)J.bands_n);
   m.base.scale_mode = uni((uint32_t)J.scale_mode);
   m.base.fmt = uni((uint32_t)J.fmt);
+  m.base.tscale = m.base.scale_mode == 1 ? *G(uni_ptr(J.scales)) : 1.0f;
   m.base.coeff = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.coeff_out)));
   m.base.cmul = uni(J.cmul);
   m.base.unit_begin = uni((uint32_t)J.unit_begin);
@@ -838,9 +842,8 @@ __device__ __forceinline__ void pm_issue_f(const PJM<KS>& M, uint32_t g0, int ti
       }
     }
   } else {
-    const float t = M.base.scale_mode == 1 ? ld_at<float>(M.base.scales, 0) : 1.0f;
 #pragma unroll
-    for (int g = 0; g < 8; ++g) f.sc[g] = t;
+    for (int g = 0; g < 8; ++g) f.sc[g] = M.base.tscale;
   }
 }
 
