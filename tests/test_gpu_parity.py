@@ -111,6 +111,29 @@ def test_fused_shapes(ctx, rows, cols, ranks, fmt, scale_mode):
     U.compare_lora_bf16(case, got)
 
 
+@pytest.mark.parametrize("coeffs", [(0.5, 1e-6, 4.0), (-3.0, 1e4, 2.0 ** -20), (1.0, 1.0, -1.0)])
+def test_fused_several_loras_coefficient_ratios(ctx, coeffs):
+    """Several LoRAs share one accumulator rescaled by c_l / c_(l+1) between
+    them; large and small ratios and equal coefficients stay within tolerance."""
+    log("case: fused ratios", coeffs)
+    ranks = tuple(zip((32, 64, 8), coeffs))
+    case = synth.tensor_case(4242, 300, 264, synth.E4M3FN, synth.SCALE_ROW, loras=ranks)
+    got = run_case(ctx, case)
+    U.compare_lora_bf16(case, got)
+
+
+@pytest.mark.parametrize("coeffs", [(1.0, 0.0), (2.0 ** -30, 1.0), (1.0, 2.0 ** 40), (3.0, -(2.0 ** 25))])
+def test_several_loras_extreme_coefficients_use_reference_order(ctx, coeffs):
+    """A zero or extreme coefficient next to another LoRA is routed to the
+    reference-order kernel (no rescaling by c_l / c_(l+1)), so the
+    result is the oracle's bit for bit."""
+    log("case: extreme coefficients", coeffs)
+    ranks = tuple(zip((32, 128), coeffs))
+    case = synth.tensor_case(4343, 300, 520, synth.E5M2, synth.SCALE_ROW, loras=ranks)
+    got = run_case(ctx, case)
+    assert np.array_equal(got.view(np.uint16), U.oracle_bf16(case).view(np.uint16))
+
+
 def test_fused_f32_output(ctx):
     """f32 output (the reference's own HostTensor type): within the f32
     forward-error bound of both orders, 2*(rank+4)*2^-24*(|deq|+sum|cBA|)."""
