@@ -220,7 +220,7 @@ def model_dir(need_bytes):
     raise SystemExit(f"no directory with {need_bytes / 1e9:.1f} GB free for the model files")
 
 
-def run_model(name, reps, warmup, log_prefix=""):
+def run_model(name, reps, warmup, log_prefix="", host_threads=8):
     """Whole-model materialisation: seeded FP8 checkpoint + LoRA files on
     disk, then per step: WeightStore.open (mmap, header parse, key rules) ->
     LoraFile.open + merge_lora -> materialize every linear into resident bf16
@@ -253,7 +253,7 @@ def run_model(name, reps, warmup, log_prefix=""):
 
         keys = [k for k, *_ in layout]
         ctx = lw.Context(0)
-        ctx.set_host_threads(min(8, threads))
+        ctx.set_host_threads(min(host_threads, threads))
         offs, total = [], 0
         for _, _, _, r, c in layout:
             offs.append(total)
@@ -331,7 +331,7 @@ def run_model(name, reps, warmup, log_prefix=""):
 
 
 def main_model(args):
-    res = run_model(args.workload, args.steps, args.warmup)
+    res = run_model(args.workload, args.steps, args.warmup, host_threads=args.host_threads)
     line = {
         "metric": METRIC,
         "value": res["s"],
@@ -364,6 +364,8 @@ def main():
                     help="whole-model materialisation reported beside the kernel workload "
                          "(auto: the 22B set beside the default layer workload, none otherwise)")
     ap.add_argument("--e2e-steps", type=int, default=3)
+    ap.add_argument("--host-threads", type=int, default=8,
+                    help="host threads filling the pinned staging block in whole-model runs")
     ap.add_argument("--exact", action="store_true",
                     help="LoRA deltas in the reference's operation order (LTXW_DESC_EXACT, bit-identical)")
     args = ap.parse_args()
@@ -473,7 +475,7 @@ def main():
     if args.e2e != "none":
         log(f"whole-model materialisation ({args.e2e})")
         try:
-            e2e = run_model(args.e2e, args.e2e_steps, 1, log_prefix="  ")
+            e2e = run_model(args.e2e, args.e2e_steps, 1, log_prefix="  ", host_threads=args.host_threads)
             if cpu is not None:
                 # The oracle's rate on this box applied to the model's device bytes.
                 e2e["cpu_estimate_s"] = round(e2e["device_bytes"] / (cpu["value"] * 1e9), 1)
