@@ -459,3 +459,66 @@ def test_mixed_factor_types_on_one_tensor(ctx, tmp):
     want = O.read_f32(w, O.E4M3FN, O.SCALE_ROW, sc, [(b1, a1, O.BF16, O.lora_coeff(1.0, None, 16)),
                                                      (b2, a2, O.F32, O.lora_coeff(0.5, None, 8))])
     assert np.array_equal(bits(store.read("x.weight", ctx)[1]), bits(want))
+
+
+def test_materialise_small_staging_slots_many_tensors(tmp):
+    """Staging slots of 12 KiB: pieces of the batch layout span several small
+    tensors (scales and factors included) and large tensors span several
+    pieces. Every tensor must come out as the oracle's: bit-exact on the
+    reference-order paths, within tolerance on the MFMA path."""
+    log("small staging slots")
+    rng = np.random.default_rng(31)
+    spec = [  # key, base dtype, shape, scale, LoRA rank (bf16 file) or None, f16 LoRA rank or None
+        ("a", "F8_E4M3", (64, 256), "row", 16, None),
+        ("b", "F8_E5M2", (3, 8), "tensor", None, None),
+        ("c", "BF16", (20, 40), None, None, None),
+        ("d", "F8_E4M3", (100, 72), "row", 8, None),
+        ("e", "F32", (7, 9), None, None, 2),
+        ("f", "F8_E4M3", (1, 8), None, None, None),
+        ("g", "F8_E5M2", (130, 264), "row", 32, None),
+        ("h", "F8_E4M3", (5, 4104), "tensor", None, None),
+        ("i", "F16", (33, 17), None, 4, None),
+    ]
+    ts, l1, l2, info = [], [], [], {}
+    for key, dt, (rows, cols), scale, r1, r2 in spec:
+        w = base_bits(rng, dt, (rows, cols))
+        ts.append((f"{key}.weight", dt, [rows, cols], w))
+        sc = None
+        if scale == "row":
+            sc = rng.uniform(1e-3, 1e-1, rows).astype(np.float32)
+            ts.append((f"{key}.weight_scale", "F32", [rows], sc))
+        elif scale == "tensor":
+            sc = rng.uniform(1e-3, 1e-1, 1).astype(np.float32)
+            ts.append((f"{key}.weight_scale", "F32", [], sc))
+        loras = []
+        for files, r, fdt, strength in ((l1, r1, "BF16", 1.0), (l2, r2, "F16", 0.75)):
+            if r is None:
+                continue
+            a = factor_bits(rng, fdt, (r, cols), 0.05)
+            b = factor_bits(rng, fdt, (rows, r), 0.05)
+            files += [(f"{key}.lora_A.weight", fdt, [r, cols], a), (f"{key}.lora_B.weight", fdt, [rows, r], b)]
+            loras.append((b.reshape(rows, r), a.reshape(r, cols), FACTOR_DT[fdt], O.lora_coeff(strength, None, r)))
+        info[key] = (w.reshape(rows, cols), dt, scale, sc, loras)
+    store = WeightStore.open([tmp(ts)])
+    store.merge_lora(LoraFile.open(tmp(l1)), 1.0)
+    store.merge_lora(LoraFile.open(tmp(l2)), 0.75)
+    keys = [f"{k}.weight" for k, *_ in spec]
+    with lw.Context(0, staging_bytes=12288, n_staging=3) as small:
+        outs = store.materialize_bf16(small, keys)
+        try:
+            for key, dt, (rows, cols), scale, r1, r2 in spec:
+                w, dt, scale, sc, loras = info[key]
+                got = outs[f"{key}.weight"].to_numpy()
+                smode = {None: O.SCALE_NONE, "row": O.SCALE_ROW, "tensor": O.SCALE_TENSOR}[scale]
+                mfma = r1 is not None and r2 is None and dt.startswith("F8") and cols % 8 == 0
+                if mfma:
+                    case = {"w": w, "scales": sc, "rows": rows, "cols": cols, "scale_mode": smode,
+                            "fmt": synth.E4M3FN if dt == "F8_E4M3" else synth.E5M2,
+                            "loras": [(b, a, b.shape[1], c) for (b, a, _, c) in loras]}
+                    U.compare_lora_bf16(case, got)
+                else:
+                    want = O.read_bf16(w, O.DTYPE_CODES[dt], smode, sc, loras)
+                    assert np.array_equal(got.view(np.uint16), want.view(np.uint16)), key
+        finally:
+            for t in outs.values():
+                t.free()
