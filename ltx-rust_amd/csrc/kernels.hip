@@ -121,8 +121,13 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* G(T* p) {
 
 // Workgroups are dispatched round-robin over the 8 XCDs; map them so that each
 // XCD takes a contiguous range of logical tiles (tiles of one row band share
-// their LoRA B rows in that XCD's L2). A bijection on [0, n).
+// their LoRA B rows in that XCD's L2). A bijection on [0, n). Launches of up
+// to kRemapMinGrid workgroups (a few layers, resident at once or nearly)
+// keep the dispatch order: measured 2-5% faster there (one 4096 x 4096 layer
+// 12.5 -> 11.9 us), while the remap wins from about a DiT block up.
+constexpr uint32_t kRemapMinGrid = 2048;
 __device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t n) {
+  if (n <= kRemapMinGrid) return bid;
   constexpr uint32_t kXcd = 8;
   uint32_t per = n / kXcd, rem = n % kXcd;
   uint32_t x = bid % kXcd, k = bid / kXcd;
