@@ -241,6 +241,16 @@ int run_exact(ltxw_ctx* ctx, const ltxw_tensor_desc& d, const ltxw::DescEx* ex) 
 
 // Dequant without LoRA: vector kernel on 16-element chunks, generic on the rest.
 int run_dequant(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t n) {
+  // Tensors up to one layer's size: the tiled kernel (one launch resident at
+  // once, both units' bytes requested up front).
+  if (n <= ltxw::kTileMaxElems && d.cols % 8 == 0 && aligned(d.w, 16) && aligned(d.out, 16) &&
+      (d.scale_mode != LTXW_SCALE_ROW || aligned(d.scales, 16))) {
+    ltxw::DequantTileArgs a{d.w, d.out, d.scales, (uint32_t)d.rows, (uint32_t)d.cols,
+                            (uint32_t)((d.cols + ltxw::kBandCols - 1) / ltxw::kBandCols)};
+    HIP_TRY(ctx, ltxw::launch_dequant_tile(a, d.fmt, d.scale_mode, d.out_dtype == LTXW_OUT_F32, ctx->compute),
+            "tiled dequant kernel launch");
+    return LTXW_OK;
+  }
   bool vec = aligned(d.w, 16) && aligned(d.out, 16) && (d.scale_mode != LTXW_SCALE_ROW || d.cols >= 16);
   uint64_t chunks = vec ? n / 16 : 0;
   if (chunks) {

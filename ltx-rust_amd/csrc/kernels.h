@@ -113,6 +113,21 @@ hipError_t launch_exact(const ExactArgs& a, bool f32out, hipStream_t stream);
 hipError_t launch_dequant(const DequantArgs& a, int fmt, int scale_mode, bool f32out,
                           hipStream_t stream);
 
+// Tiled dequant for tensors of up to kTileMaxElems elements: the fused
+// kernels' access pattern (pairs of 128-row x 128-column units per
+// workgroup, 8 FP8 bytes per lane and row) without the LoRA. Requirements
+// checked by the caller: cols % 8 == 0; w, out (and row scales) 16-byte
+// aligned; rows * cols * 4 < 2^32.
+struct DequantTileArgs {
+  const uint8_t* w;
+  void* out;
+  const float* scales;
+  uint32_t rows, cols, bands_n;
+};
+constexpr uint64_t kTileMaxElems = 1ull << 25;
+hipError_t launch_dequant_tile(const DequantTileArgs& a, int fmt, int scale_mode, bool f32out,
+                               hipStream_t stream);
+
 // Fused dequant + LoRA over every work unit of every job. Requirements checked
 // by the caller: cols % 8 == 0, ranks % 8 == 0, all pointers 16-byte aligned,
 // total padded rank <= kRankMax, the same K-steps for every job

@@ -925,6 +925,127 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   }
 }
 
+// ---------------------------------------------------------------------------
+// (a') Tiled dequant: the fused kernels' tile walk and lane layout without
+// the LoRA. A workgroup takes two vertically adjacent 128 x 128 units of a
+// column band; lane l of wave w handles, in each unit, the 8 columns
+// i0 + 8 (l % 16) .. +7 of rows r0 + 4 (l / 16) + {0..3, 16..19} with
+// r0 = g0 + 32 w. Both units' bytes are requested before the first unit is
+// converted. Faster than the streaming kernel on tensors of one layer's size
+// (a launch that is resident at once); the streaming kernel wins on larger
+// ones.
+// ---------------------------------------------------------------------------
+template <int SMODE, bool FULL>
+__device__ __forceinline__ void dqt_load(const DequantTileArgs& a, uint32_t i0, uint32_t g0, int tid, u32x2 (&wv)[8],
+                                         float (&sc)[8], float tscale) {
+  const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
+  const uint32_t rl = g0 + kStripRows * wave + 4 * lg;
+  const uint32_t ecol = i0 + 8 * ln;
+  const bool col_ok = FULL || ecol < a.cols;
+  const uint32_t e0 = rl * a.cols + ecol;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    const uint32_t dr = 16 * (g >> 2) + (g & 3);
+    wv[g] = (u32x2){0u, 0u};
+    if (col_ok && (FULL || rl + dr < a.rows)) wv[g] = ld_nt_at<u32x2>(a.w, e0 + dr * a.cols);
+  }
+  if (SMODE == 2) {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const uint32_t rb = rl + 16 * mb;
+      if (FULL || rb + 3 < a.rows) {
+        const f32x4 q = ld_at<f32x4>(a.scales, 4 * rb);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sc[4 * mb + v] = q[v];
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sc[4 * mb + v] = rb + v < a.rows ? ld_at<float>(a.scales, 4 * (rb + v)) : 1.0f;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < 8; ++g) sc[g] = tscale;
+  }
+}
+
+template <int FMT, int SMODE, bool F32OUT, bool FULL>
+__device__ __forceinline__ void dqt_store(const DequantTileArgs& a, uint32_t i0, uint32_t g0, int tid,
+                                          const u32x2 (&wv)[8], const float (&sc)[8]) {
+  const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
+  const uint32_t rl = g0 + kStripRows * wave + 4 * lg;
+  const uint32_t ecol = i0 + 8 * ln;
+  const bool col_ok = FULL || ecol < a.cols;
+  const uint32_t e0 = rl * a.cols + ecol;
+  float x[8][8];
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    decode4(wv[g][0], FMT, x[g]);
+    decode4(wv[g][1], FMT, x[g] + 4);
+    if (SMODE != 0) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[g][j] = __builtin_fmaf(sc[g], x[g][j], 0.0f);
+    }
+  }
+  canon_nan_wave<64>(&x[0][0]);
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    const uint32_t dr = 16 * (g >> 2) + (g & 3);
+    if (!(col_ok && (FULL || rl + dr < a.rows))) continue;
+    const uint32_t e = e0 + dr * a.cols;
+    if (F32OUT) {
+      st_nt_at<f32x4>(a.out, 4 * e, (f32x4){x[g][0], x[g][1], x[g][2], x[g][3]});
+      st_nt_at<f32x4>(a.out, 4 * e + 16, (f32x4){x[g][4], x[g][5], x[g][6], x[g][7]});
+    } else {
+      const u32x4 o = {pack_bf16(x[g][0], x[g][1]), pack_bf16(x[g][2], x[g][3]), pack_bf16(x[g][4], x[g][5]),
+                       pack_bf16(x[g][6], x[g][7])};
+      st_nt_at<u32x4>(a.out, 2 * e, o);
+    }
+  }
+}
+
+template <int FMT, int SMODE, bool F32OUT, bool FULL>
+__device__ __forceinline__ void dqt_pair(const DequantTileArgs& a, uint32_t i0, uint32_t gA, uint32_t gB, bool hasB,
+                                         int tid, float tscale) {
+  u32x2 wa[8], wb[8];
+  float sa[8], sb[8];
+  dqt_load<SMODE, FULL>(a, i0, gA, tid, wa, sa, tscale);
+  if (hasB) dqt_load<SMODE, FULL>(a, i0, gB, tid, wb, sb, tscale);
+  dqt_store<FMT, SMODE, F32OUT, FULL>(a, i0, gA, tid, wa, sa);
+  if (hasB) dqt_store<FMT, SMODE, F32OUT, FULL>(a, i0, gB, tid, wb, sb);
+}
+
+template <int FMT, int SMODE, bool F32OUT>
+__global__ __launch_bounds__(256) void k_dequant_tile(DequantTileArgs a) {
+  const int tid = threadIdx.x;
+  const uint32_t p = blockIdx.x;
+  const uint32_t i0 = (p % a.bands_n) * kBandCols;
+  const uint32_t gA = (p / a.bands_n) * kPairRows;
+  const uint32_t gB = gA + kWavesPerGroup * kStripRows;
+  const bool hasB = gB < a.rows;
+  const bool full = gA + kPairRows <= a.rows && i0 + kBandCols <= a.cols;
+  const float tscale = SMODE == 1 ? *G(uni_ptr(a.scales)) : 1.0f;
+  if (full) dqt_pair<FMT, SMODE, F32OUT, true>(a, i0, gA, gB, hasB, tid, tscale);
+  else dqt_pair<FMT, SMODE, F32OUT, false>(a, i0, gA, gB, hasB, tid, tscale);
+}
+
+template <int FMT, int SMODE>
+hipError_t dequant_tile_out(const DequantTileArgs& a, bool f32out, dim3 grid, hipStream_t s) {
+  if (f32out)
+    hipLaunchKernelGGL((k_dequant_tile<FMT, SMODE, true>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((k_dequant_tile<FMT, SMODE, false>), grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int FMT>
+hipError_t dequant_tile_scale(const DequantTileArgs& a, int smode, bool f32out, dim3 grid, hipStream_t s) {
+  switch (smode) {
+    case 0: return dequant_tile_out<FMT, 0>(a, f32out, grid, s);
+    case 1: return dequant_tile_out<FMT, 1>(a, f32out, grid, s);
+    default: return dequant_tile_out<FMT, 2>(a, f32out, grid, s);
+  }
+}
+
 template <int FMT, int SMODE>
 hipError_t dequant_dispatch_out(const DequantArgs& a, bool f32out, dim3 grid, hipStream_t s) {
   if (f32out)
@@ -952,6 +1073,15 @@ hipError_t launch_dequant(const DequantArgs& a, int fmt, int scale_mode, bool f3
   dim3 grid((unsigned)((a.n_chunks + per_block - 1) / per_block));
   return fmt == 0 ? dequant_dispatch_scale<0>(a, scale_mode, f32out, grid, stream)
                   : dequant_dispatch_scale<1>(a, scale_mode, f32out, grid, stream);
+}
+
+hipError_t launch_dequant_tile(const DequantTileArgs& a, int fmt, int scale_mode, bool f32out,
+                               hipStream_t stream) {
+  const uint64_t pairs = (uint64_t)a.bands_n * ((a.rows + kPairRows - 1) / kPairRows);
+  if (pairs == 0) return hipSuccess;
+  dim3 grid((unsigned)pairs);
+  return fmt == 0 ? dequant_tile_scale<0>(a, scale_mode, f32out, grid, stream)
+                  : dequant_tile_scale<1>(a, scale_mode, f32out, grid, stream);
 }
 
 template <int KS>
