@@ -41,6 +41,8 @@ ROTATE_BYTES = 1 << 30
 PMC_SUMMARY = {
     "layer": os.path.join(ROOT, "profiles", "k_fused_pair_layer4096x4096_r64.pmc.txt"),
     "block": os.path.join(ROOT, "profiles", "k_fused_pair_ditblock_r64.pmc.txt"),
+    "dequant": os.path.join(ROOT, "profiles", "k_dequant_tile_layer4096x4096.pmc.txt"),
+    "mixed": os.path.join(ROOT, "profiles", "k_fused_pair_multi_mixedblock_r32_r128.pmc.txt"),
 }
 
 
