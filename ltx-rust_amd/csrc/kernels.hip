@@ -329,12 +329,15 @@ __global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
             As[tid >> 3][cc + q] = (rr < rank && ii < cols) ? factor_at<FDT>(L.a, L.dtype, rr * cols + ii) : 0.0f;
           }
         }
+        // Bs holds c = coeff * B[o][r], rounded to f32 once here, exactly
+        // as the reference forms it before each row's FMA pass.
         const uint64_t oo = g0 + (tid >> 2);
         const int q0 = (tid & 3) * 8;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
           const uint64_t rq = r0 + q0 + q;
-          Bs[tid >> 2][q0 + q] = (oo < rows && rq < rank) ? factor_at<FDT>(L.b, L.dtype, oo * rank + rq) : 0.0f;
+          Bs[tid >> 2][q0 + q] =
+              (oo < rows && rq < rank) ? L.coeff * factor_at<FDT>(L.b, L.dtype, oo * rank + rq) : 0.0f;
         }
       }
       __syncthreads();
@@ -348,7 +351,7 @@ __global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
         const float a[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const float c = L.coeff * Bs[rs + 16 * k][r];
+          const float c = Bs[rs + 16 * k][r];
 #pragma unroll
           for (int j = 0; j < 8; ++j) acc[k][j] = __builtin_fmaf(c, a[j], acc[k][j]);
         }
