@@ -222,7 +222,7 @@ def model_dir(need_bytes):
     raise SystemExit(f"no directory with {need_bytes / 1e9:.1f} GB free for the model files")
 
 
-def run_model(name, reps, warmup, log_prefix="", host_threads=8):
+def run_model(name, reps, warmup, log_prefix="", host_threads=8, staging_mib=0, staging_slots=0):
     """Whole-model materialisation: seeded FP8 checkpoint + LoRA files on
     disk, then per step: WeightStore.open (mmap, header parse, key rules) ->
     LoraFile.open + merge_lora -> materialize every linear into resident bf16
@@ -254,7 +254,7 @@ def run_model(name, reps, warmup, log_prefix="", host_threads=8):
         log(f"{log_prefix}wrote {h2d_bytes / 1e9:.1f} GB of files to {d} in {res['write_s']} s")
 
         keys = [k for k, *_ in layout]
-        ctx = lw.Context(0)
+        ctx = lw.Context(0, staging_bytes=staging_mib << 20, n_staging=staging_slots)
         ctx.set_host_threads(min(host_threads, threads))
         offs, total = [], 0
         for _, _, _, r, c in layout:
@@ -333,7 +333,8 @@ def run_model(name, reps, warmup, log_prefix="", host_threads=8):
 
 
 def main_model(args):
-    res = run_model(args.workload, args.steps, args.warmup, host_threads=args.host_threads)
+    res = run_model(args.workload, args.steps, args.warmup, host_threads=args.host_threads,
+                    staging_mib=args.staging_mib, staging_slots=args.staging_slots)
     line = {
         "metric": METRIC,
         "value": res["s"],
@@ -368,6 +369,10 @@ def main():
     ap.add_argument("--e2e-steps", type=int, default=3)
     ap.add_argument("--host-threads", type=int, default=8,
                     help="host threads filling the pinned staging block in whole-model runs")
+    ap.add_argument("--staging-mib", type=int, default=0,
+                    help="pinned staging slot size in MiB for whole-model runs (0: the library default, 64)")
+    ap.add_argument("--staging-slots", type=int, default=0,
+                    help="pinned staging slots for whole-model runs (0: the library default, 16)")
     ap.add_argument("--exact", action="store_true",
                     help="LoRA deltas in the reference's operation order (LTXW_DESC_EXACT, bit-identical)")
     args = ap.parse_args()
@@ -477,7 +482,8 @@ def main():
     if args.e2e != "none":
         log(f"whole-model materialisation ({args.e2e})")
         try:
-            e2e = run_model(args.e2e, args.e2e_steps, 1, log_prefix="  ", host_threads=args.host_threads)
+            e2e = run_model(args.e2e, args.e2e_steps, 1, log_prefix="  ", host_threads=args.host_threads,
+                            staging_mib=args.staging_mib, staging_slots=args.staging_slots)
             if cpu is not None:
                 # The oracle's rate on this box applied to the model's device bytes.
                 e2e["cpu_estimate_s"] = round(e2e["device_bytes"] / (cpu["value"] * 1e9), 1)
