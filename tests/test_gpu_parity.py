@@ -221,6 +221,34 @@ def test_dit_block_sampled_rows(ctx):
             d.free()
 
 
+def test_mixed_format_block_sampled_rows(ctx):
+    """The mixed-format DiT block at full size in one grouped call: attention
+    e4m3fn with one scale, FFN e5m2 with row scales, the 4096 x 4104 and
+    4104 x 16384 edge tensors, and two stacked LoRAs (rank 32, coefficient 1;
+    rank 128, coefficient 0.5) on every tensor; 48 sampled rows plus the first
+    and last of each tensor against the oracle."""
+    log("case: mixed-format block")
+    rng = np.random.default_rng(5)
+    shapes = [(nm, r, c, nm.startswith("ff.")) for nm, r, c in synth.BLOCK_LINEARS]
+    shapes += [("edge.proj_a", 4096, 4104, False), ("edge.proj_b", 4104, 16384, True)]
+    cases, devs = [], []
+    try:
+        for k, (name, rows, cols, ffn) in enumerate(shapes):
+            fmt, sm = (synth.E5M2, synth.SCALE_ROW) if ffn else (synth.E4M3FN, synth.SCALE_TENSOR)
+            c = synth.tensor_case(5000 + k, rows, cols, fmt, sm, loras=((32, 1.0), (128, 0.5)))
+            cases.append(c)
+            devs.append(U.Dev(ctx, c))
+        ctx.grouped([{"w": d.w, "out": d.out, "scales": d.s, "rows": d.case["rows"], "cols": d.case["cols"],
+                      "fmt": d.case["fmt"], "scale_mode": d.case["scale_mode"], "loras": d.loras} for d in devs])
+        for d, c in zip(devs, cases):
+            got = d.result()
+            sel = np.unique(np.concatenate([[0, c["rows"] - 1], rng.choice(c["rows"], 48, replace=False)]))
+            U.compare_lora_bf16(c, got[sel], row_sel=sel)
+    finally:
+        for d in devs:
+            d.free()
+
+
 def test_invalid_arguments_report_status(ctx):
     log("case: errors")
     p = ctx.alloc(1024)
