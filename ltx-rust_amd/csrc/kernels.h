@@ -137,6 +137,10 @@ hipError_t launch_dequant_tile(const DequantTileArgs& a, int fmt, int scale_mode
 // coeff_out and step[] are filled (plan_fused in api.cpp).
 hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, hipStream_t stream);
 
+// The several-LoRA kernel alone (kernels_multi.hip); `ks` K-steps (1-7).
+// launch_fused calls it for `multi`.
+hipError_t launch_fused_multi(const JobTable& t, bool f32out, int ks, hipStream_t stream);
+
 // Rows of one workgroup of the single-LoRA kernel.
 constexpr int kPairRows = 2 * kWavesPerGroup * kStripRows;
 

@@ -8,131 +8,10 @@
 // The hardware FP8 converts equal the closed form of fp8.rs:90-158 on every
 // finite and infinite code; for NaN codes they return 0xFFC00000 where the
 // reference returns f32::NAN (0x7FC00000), so NaN results are canonicalised.
-#include "kernels.h"
+#include "kernels_dev.h"
 
 namespace ltxw {
 namespace {
-
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
-constexpr uint32_t kCanonNaN = 0x7FC00000u;
-
-__device__ __forceinline__ float canon_nan(float x) {
-  return __builtin_isnan(x) ? __builtin_bit_cast(float, kCanonNaN) : x;
-}
-
-// Canonicalise the NaNs among n values, paying only a compare per value when
-// the whole wave holds none (the usual case): the per-value NaN tests are
-// combined into one wave-wide mask, and the selects run only if it is set.
-template <int N>
-__device__ __forceinline__ void canon_nan_wave(float* v) {
-  uint64_t any = 0;
-#pragma unroll
-  for (int j = 0; j < N; ++j) any |= __builtin_amdgcn_ballot_w64(__builtin_isnan(v[j]));
-  if (any) {
-#pragma unroll
-    for (int j = 0; j < N; ++j) v[j] = canon_nan(v[j]);
-  }
-}
-
-__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  bf16x2 r = __builtin_convertvector((f32x2){a, b}, bf16x2);
-  return __builtin_bit_cast(uint32_t, r);
-}
-
-// Four FP8 bytes of `word` (little-endian) -> four f32.
-__device__ __forceinline__ void decode4(uint32_t word, int fmt, float* v) {
-  f32x2 lo, hi;
-  if (fmt == 0) {
-    lo = __builtin_amdgcn_cvt_pk_f32_fp8(word, false);
-    hi = __builtin_amdgcn_cvt_pk_f32_fp8(word, true);
-  } else {
-    lo = __builtin_amdgcn_cvt_pk_f32_bf8(word, false);
-    hi = __builtin_amdgcn_cvt_pk_f32_bf8(word, true);
-  }
-  v[0] = lo[0];
-  v[1] = lo[1];
-  v[2] = hi[0];
-  v[3] = hi[1];
-}
-
-__device__ __forceinline__ float decode1(uint32_t byte, int fmt) {
-  float v[4];
-  decode4(byte, fmt, v);
-  return v[0];
-}
-
-__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
-  return __builtin_bit_cast(float, (uint32_t)h << 16);
-}
-
-// IEEE binary16 -> f32, exact; a NaN keeps sign and payload and gets the
-// quiet bit (as `half`'s f16::to_f32, store.rs:690-705).
-__device__ __forceinline__ float f16_to_f32(uint16_t h) {
-  if ((h & 0x7C00u) == 0x7C00u && (h & 0x3FFu))
-    return __builtin_bit_cast(float, ((uint32_t)(h & 0x8000u) << 16) | 0x7FC00000u | ((uint32_t)(h & 0x3FFu) << 13));
-  return (float)__builtin_bit_cast(_Float16, h);
-}
-
-// f32 -> bf16, round to nearest even; a NaN keeps sign and the top payload
-// bits and gets the quiet bit (half's bf16::from_f32).
-__device__ __forceinline__ uint16_t bf16_rne(float v) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, v);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
-  return (uint16_t)(pack_bf16(v, 0.0f) & 0xFFFFu);
-}
-
-// Element e of a LoRA factor of element type dt (0 bf16, 1 f32, 2 f16,
-// 3 e4m3fn, 4 e5m2), widened exactly as lora.rs:176-209 does.
-__device__ __forceinline__ float load_factor(const void* p, int dt, uint64_t e) {
-  switch (dt) {
-    case 0: return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[e]);
-    case 1: return reinterpret_cast<const float*>(p)[e];
-    case 2: return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[e]);
-    default: return canon_nan(decode1(reinterpret_cast<const uint8_t*>(p)[e], dt - 3));
-  }
-}
-
-// Element e of a base tensor in any of the accepted formats
-// (0 e4m3fn, 1 e5m2, 2 bf16, 3 f16, 4 f32; store.rs:672-729).
-__device__ __forceinline__ float load_base(const JobDev& J, uint64_t e) {
-  switch (J.fmt) {
-    case 0:
-    case 1: return canon_nan(decode1(J.w[e], J.fmt));
-    case 2: return bf16_to_f32(reinterpret_cast<const uint16_t*>(J.w)[e]);
-    case 3: return f16_to_f32(reinterpret_cast<const uint16_t*>(J.w)[e]);
-    default: return reinterpret_cast<const float*>(J.w)[e];
-  }
-}
-
-// Pointers read out of job descriptors are generic; marking them global makes
-// the compiler emit global_load/global_store (not flat_*, which also count
-// against the LDS counter and skip the global addressing modes).
-template <typename T>
-__device__ __forceinline__ __attribute__((address_space(1))) T* G(T* p) {
-  return (__attribute__((address_space(1))) T*)(p);
-}
-
-// Workgroups are dispatched round-robin over the 8 XCDs; map them so that each
-// XCD takes a contiguous range of logical tiles (tiles of one row band share
-// their LoRA B rows in that XCD's L2). A bijection on [0, n). Launches of up
-// to kRemapMinGrid workgroups (a few layers, resident at once or nearly)
-// keep the dispatch order: measured 2-5% faster there (one 4096 x 4096 layer
-// 12.5 -> 11.9 us), while the remap wins from about a DiT block up.
-constexpr uint32_t kRemapMinGrid = 2048;
-__device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t n) {
-  if (n <= kRemapMinGrid) return bid;
-  constexpr uint32_t kXcd = 8;
-  uint32_t per = n / kXcd, rem = n % kXcd;
-  uint32_t x = bid % kXcd, k = bid / kXcd;
-  return x < rem ? x * (per + 1) + k : rem * (per + 1) + (x - rem) * per + k;
-}
 
 // ---------------------------------------------------------------------------
 // (a) Streaming dequant. Each thread handles kChunksPerThread chunks of 16
@@ -391,313 +270,6 @@ __global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// (b) Fused dequant + LoRA merge.
-//
-// Work unit: one band of 128 output columns [i0, i0+128) by 128 rows; each of
-// a workgroup's 4 waves owns a strip of 32 rows, [r0, r0+32).
-//
-// LoRA product on v_mfma_f32_16x16x32_bf16 with M = output row o, N = output
-// column i, K = rank r, and the N index permuted as i = i0 + 8*n + nb for
-// N-block nb (0..7) and MFMA column n (0..15). With the C layout (lane l holds
-// column n = l%16 and rows m = 4*(l/16) + v), lane l then owns, for each of
-// its 8 rows, the 8 contiguous columns i0 + 8*(l%16) .. +7 across the 8
-// N-blocks: the FP8 input (8 bytes per lane) and the bf16 output (16 bytes per
-// lane) go straight between registers and HBM, 16 lanes covering 128
-// contiguous columns of a row, with no LDS relayout.
-//   A operand (o x r): LoRA B rows, 16-byte loads (r contiguous), from L2.
-//   B operand (r x i): LoRA A transposed, staged per work unit in LDS as
-//                      AT[slot][k] with slot = nb*16 + n (consecutive lanes
-//                      read consecutive slots: conflict-free 128-bit reads).
-// Several LoRAs are staged side by side along k (each padded to 32).
-//
-// Issue order is latency order: the L2-resident factor loads (A for the LDS
-// stage, then every B fragment) go out first, the FP8 bytes and scales from
-// HBM last. Loads retire in order, so staging, the barrier and the MFMAs run
-// while the HBM data is still in flight.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ void load_job(const JobTable& t, uint64_t unit, JobDev& J) {
-  if (t.n_jobs == 1) {
-    J = t.one;
-    return;
-  }
-  int lo = 0, hi = t.n_jobs - 1;  // last job with begins[j] <= unit
-  while (lo < hi) {
-    int mid = (lo + hi + 1) >> 1;
-    if ((uint64_t)G(t.begins)[mid] <= unit) lo = mid; else hi = mid - 1;
-  }
-  // Copy the descriptor as 16-byte global loads (the table is 256-byte aligned).
-  static_assert(sizeof(JobDev) % 16 == 0, "JobDev is copied in 16-byte pieces");
-  u32x4 raw[sizeof(JobDev) / 16];
-  const auto src = G(reinterpret_cast<const u32x4*>(t.jobs + lo));
-#pragma unroll
-  for (int k = 0; k < (int)(sizeof(JobDev) / 16); ++k) raw[k] = src[k];
-  __builtin_memcpy(&J, raw, sizeof(JobDev));
-}
-
-// Loads and stores at a 32-bit byte offset from a wave-uniform base pointer,
-// so the compiler can use the SGPR-base + VGPR-offset addressing mode (one
-// VGPR of address per lane, no 64-bit address arithmetic). The host routes
-// tensors whose byte extents do not fit 32 bits to the generic kernel.
-template <typename T>
-__device__ __forceinline__ T ld_at(const void* base, uint32_t off) {
-  return *reinterpret_cast<const __attribute__((address_space(1))) T*>(
-      (const __attribute__((address_space(1))) char*)base + off);
-}
-template <typename T>
-__device__ __forceinline__ T ld_nt_at(const void* base, uint32_t off) {
-  return __builtin_nontemporal_load(reinterpret_cast<const __attribute__((address_space(1))) T*>(
-      (const __attribute__((address_space(1))) char*)base + off));
-}
-template <typename T>
-__device__ __forceinline__ void st_nt_at(void* base, uint32_t off, T v) {
-  __builtin_nontemporal_store(v, reinterpret_cast<__attribute__((address_space(1))) T*>(
-                                     (__attribute__((address_space(1))) char*)base + off));
-}
-
-// ---------------------------------------------------------------------------
-// (b') Workgroup schedule: two vertically adjacent work units of one band per
-// workgroup, in straight-line code. A^T is staged once for both; the second
-// unit's FP8 bytes are requested with the first unit's, and its L2-resident
-// factor loads go out while the first unit's epilogue runs, so the second
-// unit's HBM latency hides behind the first unit's LoRA chain.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t uni(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
-template <typename T>
-__device__ __forceinline__ T* uni_ptr(T* p) {
-  const uint64_t v = (uint64_t)p;
-  return (T*)(((uint64_t)uni((uint32_t)(v >> 32)) << 32) | uni((uint32_t)v));
-}
-
-// The fields of one single-LoRA job the pipelined kernel uses, wave-uniform.
-struct PJ {
-  const uint8_t* w;
-  void* out;
-  const float* scales;
-  const uint16_t* a;
-  const uint16_t* b;
-  uint32_t rows, cols, rank, bands_n, scale_mode, fmt;
-  float coeff;
-  uint32_t cmul;  // coeff applies (coeff != 1)
-  uint32_t unit_begin;
-  float tscale;   // the per-tensor scale (scale_mode 1), else 1
-};
-
-__device__ __forceinline__ PJ pj_load(const JobTable& t, uint64_t unit) {
-  JobDev J;
-  load_job(t, unit, J);
-  PJ p;
-  p.w = uni_ptr(J.w);
-  p.out = uni_ptr(J.out);
-  p.scales = uni_ptr(J.scales);
-  p.a = uni_ptr(J.lora[0].a);
-  p.b = uni_ptr(J.lora[0].b);
-  p.rows = uni((uint32_t)J.rows);
-  p.cols = uni((uint32_t)J.cols);
-  p.rank = uni((uint32_t)J.lora[0].rank);
-  p.bands_n = uni((uint32_t)J.bands_n);
-  p.scale_mode = uni((uint32_t)J.scale_mode);
-  p.fmt = uni((uint32_t)J.fmt);
-  // One uniform load at the start: no per-lane load in the scale branch of
-  // the factor issue (a vector load on one path only costs waits on both).
-  p.tscale = p.scale_mode == 1 ? *G(uni_ptr(J.scales)) : 1.0f;
-  p.coeff = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.coeff_out)));
-  p.cmul = uni(J.cmul);
-  p.unit_begin = uni((uint32_t)J.unit_begin);
-  return p;
-}
-
-template <int KS>
-struct Frag {
-  bf16x8 bf[KS][2];
-  u32x2 wv[8];
-  float sc[8];
-};
-template <int KS>
-struct Stage {
-  u32x4 lo[KS], hi[KS];
-};
-
-// A^T staging: for K-step t, thread tid loads ranks 32 t + 2 (tid % 16) and
-// +1 of A for the 8 columns i0 + 8 (tid / 16) .. +7 and stores them into
-// AT[slot][32 t + ..] with slot = (i % 8) * 16 + i / 8 for local column i.
-template <int KS>
-__device__ __forceinline__ void pp_issue_a(const PJ& J, uint32_t i0, int tid, Stage<KS>& st) {
-  const int sq = tid & 15;
-  const uint32_t scol = i0 + 8 * (tid >> 4);
-  const bool scol_ok = scol < J.cols;
-#pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    const uint32_t k = 32 * t + 2 * sq;
-    st.lo[t] = (u32x4){0u, 0u, 0u, 0u};
-    st.hi[t] = st.lo[t];
-    if (scol_ok && k < J.rank) st.lo[t] = ld_at<u32x4>(J.a, 2 * (k * J.cols + scol));
-    if (scol_ok && k + 1 < J.rank) st.hi[t] = ld_at<u32x4>(J.a, 2 * ((k + 1) * J.cols + scol));
-  }
-}
-
-template <int KS, bool FULL>
-__device__ __forceinline__ void pp_issue_f(const PJ& J, uint32_t i0, uint32_t g0, int tid, Frag<KS>& f) {
-  const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
-  const uint32_t rows = J.rows;
-  const uint32_t r0 = g0 + kStripRows * wave;
-#pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    const uint32_t kk = 32 * t + 8 * lg;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      const uint32_t ob = r0 + 16 * mb + ln;
-      f.bf[t][mb] = (bf16x8){};
-      if (kk < J.rank && (FULL || ob < rows)) f.bf[t][mb] = ld_at<bf16x8>(J.b, 2 * (ob * J.rank + kk));
-    }
-  }
-  const uint32_t rl = r0 + 4 * lg;
-  if (J.scale_mode == 2) {
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      const uint32_t rb = rl + 16 * mb;
-      if (FULL || rb + 3 < rows) {
-        const f32x4 q = ld_at<f32x4>(J.scales, 4 * rb);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) f.sc[4 * mb + v] = q[v];
-      } else {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) f.sc[4 * mb + v] = rb + v < rows ? ld_at<float>(J.scales, 4 * (rb + v)) : 1.0f;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int g = 0; g < 8; ++g) f.sc[g] = J.tscale;
-  }
-}
-
-template <int KS, bool FULL>
-__device__ __forceinline__ void pp_issue_w(const PJ& J, uint32_t i0, uint32_t g0, int tid, Frag<KS>& f) {
-  const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
-  const uint32_t rows = J.rows, cols = J.cols;
-  const uint32_t r0 = g0 + kStripRows * wave;
-  const uint32_t rl = r0 + 4 * lg;
-  const uint32_t ecol = i0 + 8 * ln;
-  const bool col_ok = FULL || ecol < cols;
-  const uint32_t e0 = rl * cols + ecol;
-#pragma unroll
-  for (int g = 0; g < 8; ++g) {
-    const uint32_t dr = 16 * (g >> 2) + (g & 3);
-    f.wv[g] = (u32x2){0u, 0u};
-    if (col_ok && (FULL || rl + dr < rows)) f.wv[g] = ld_nt_at<u32x2>(J.w, e0 + dr * cols);
-  }
-}
-
-template <int KS>
-__device__ __forceinline__ void pp_stage(const Stage<KS>& st, uint16_t* AT, int ld, int tid) {
-  const int sq = tid & 15;
-#pragma unroll
-  for (int t = 0; t < KS; ++t)
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      const uint32_t pair = __builtin_amdgcn_perm(st.hi[t][jj >> 1], st.lo[t][jj >> 1],
-                                                  (jj & 1) ? 0x07060302u : 0x05040100u);
-      *reinterpret_cast<uint32_t*>(&AT[(jj * 16 + (tid >> 4)) * ld + 32 * t + 2 * sq]) = pair;
-    }
-}
-
-template <int KS>
-struct Acc {
-  f32x4 v[2][8];
-};
-
-template <int KS>
-__device__ __forceinline__ void pp_mfma(const Frag<KS>& f, const uint16_t* AT, int ld, int tid, Acc<KS>& a) {
-  const int lane = tid & 63, ln = lane & 15, lg = lane >> 4;
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) a.v[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    const int kk = 32 * t + 8 * lg;
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + kk]);
-      a.v[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][0], at, a.v[0][nb], 0, 0, 0);
-      a.v[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][1], at, a.v[1][nb], 0, 0, 0);
-    }
-  }
-}
-
-template <bool F32OUT, int KS, bool FULL, int FMT>
-__device__ __forceinline__ void pp_epilogue(const PJ& J, const Frag<KS>& f, Acc<KS>& a, uint32_t i0, uint32_t g0,
-                                            int tid) {
-  const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
-  const uint32_t rows = J.rows, cols = J.cols;
-  const uint32_t r0 = g0 + kStripRows * wave;
-  const float c = J.coeff;
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
-    // A flag from the job, not a test of c: the compiler would turn
-    // `if (c != 1) v *= c` into an unconditional multiply.
-    if (J.cmul) {
-#pragma unroll
-      for (int nb = 0; nb < 8; ++nb) a.v[mb][nb] *= c;
-    }
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int g = 4 * mb + v;
-      float x[8];
-      decode4(f.wv[g][0], FMT, x);
-      decode4(f.wv[g][1], FMT, x + 4);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) a.v[mb][j][v] = __builtin_fmaf(f.sc[g], x[j], a.v[mb][j][v]);
-    }
-  }
-  {
-    uint64_t any = 0;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < 8; ++nb)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) any |= __builtin_amdgcn_ballot_w64(__builtin_isnan(a.v[mb][nb][v]));
-    if (any) {
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) a.v[mb][nb][v] = canon_nan(a.v[mb][nb][v]);
-    }
-  }
-  const uint32_t rl = r0 + 4 * lg;
-  const uint32_t ecol = i0 + 8 * ln;
-  const bool col_ok = FULL || ecol < cols;
-  const uint32_t e0 = rl * cols + ecol;
-#pragma unroll
-  for (int g = 0; g < 8; ++g) {
-    const int mb = g >> 2, v = g & 3;
-    const uint32_t dr = 16 * mb + v;
-    if (col_ok && (FULL || rl + dr < rows)) {
-      const uint32_t e = e0 + dr * cols;
-      float x[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = a.v[mb][j][v];
-      if (F32OUT) {
-        st_nt_at<f32x4>(J.out, 4 * e, (f32x4){x[0], x[1], x[2], x[3]});
-        st_nt_at<f32x4>(J.out, 4 * e + 16, (f32x4){x[4], x[5], x[6], x[7]});
-      } else {
-        const u32x4 o = {pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]), pack_bf16(x[4], x[5]), pack_bf16(x[6], x[7])};
-        st_nt_at<u32x4>(J.out, 2 * e, o);
-      }
-    }
-  }
-}
-
-template <bool F32OUT, int KS, int FMT>
-__device__ __forceinline__ void pp_epilogue_any(const PJ& J, const Frag<KS>& f, Acc<KS>& a, uint32_t i0,
-                                                uint32_t g0, int tid) {
-  if (g0 + 128 <= J.rows && i0 + 128 <= J.cols) pp_epilogue<F32OUT, KS, true, FMT>(J, f, a, i0, g0, tid);
-  else pp_epilogue<F32OUT, KS, false, FMT>(J, f, a, i0, g0, tid);
-}
-
 // Two vertically adjacent units of one band (rows [gA, gA + 256)).
 template <bool F32OUT, int KS, int FMT, bool FULL>
 __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i0, uint32_t gA, uint32_t gB,
@@ -746,185 +318,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 3
   } else {
     if (full) pair_units<F32OUT, KS, 1, true>(J, AT, i0, gA, gB, hasB, tid);
     else pair_units<F32OUT, KS, 1, false>(J, AT, i0, gA, gB, hasB, tid);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Several LoRAs per tensor, two units per workgroup. The LoRAs sit side by
-// side along K (each padded to 32) and the host describes every K-step
-// (StepDev: the step's A rows, B columns, rank and present ranks). One
-// accumulator set carries the whole delta: at the last step of LoRA l, with
-// LoRA l+1 following, the accumulator is multiplied by q = c_l / c_{l+1}, and
-// the epilogue multiplies by the last coefficient:
-//   delta = c_last (... ((B_0 A_0) q_0 + B_1 A_1) q_1 ...) = sum_l c_l B_l A_l
-// up to a few f32 roundings (the host routes coefficients whose ratios could
-// overflow or underflow to the reference-order kernel).
-// ---------------------------------------------------------------------------
-template <int KS>
-struct PJM {
-  PJ base;  // coeff / cmul: the last LoRA's coefficient
-  const uint16_t* a[KS];
-  const uint16_t* b[KS];
-  uint32_t rank[KS];
-  uint32_t klim[KS];
-  float q[KS];
-  uint32_t qmask;
-};
-
-template <int KS>
-__device__ __forceinline__ PJM<KS> pjm_load(const JobTable& t, uint64_t unit) {
-  JobDev J;
-  load_job(t, unit, J);
-  PJM<KS> m;
-  m.base.w = uni_ptr(J.w);
-  m.base.out = uni_ptr(J.out);
-  m.base.scales = uni_ptr(J.scales);
-  m.base.a = nullptr;
-  m.base.b = nullptr;
-  m.base.rows = uni((uint32_t)J.rows);
-  m.base.cols = uni((uint32_t)J.cols);
-  m.base.rank = 0;
-  m.base.bands_n = uni((uint32_t)J.bands_n);
-  m.base.scale_mode = uni((uint32_t)J.scale_mode);
-  m.base.fmt = uni((uint32_t)J.fmt);
-  m.base.tscale = m.base.scale_mode == 1 ? *G(uni_ptr(J.scales)) : 1.0f;
-  m.base.coeff = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.coeff_out)));
-  m.base.cmul = uni(J.cmul);
-  m.base.unit_begin = uni((uint32_t)J.unit_begin);
-#pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    m.a[s] = uni_ptr(J.step[s].a);
-    m.b[s] = uni_ptr(J.step[s].b);
-    m.rank[s] = uni(J.step[s].rank);
-    m.klim[s] = uni(J.step[s].klim);
-    m.q[s] = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.step[s].q)));
-  }
-  m.qmask = uni(J.qmask);
-  return m;
-}
-
-template <int KS>
-__device__ __forceinline__ void pm_issue_a(const PJM<KS>& M, uint32_t i0, int tid, Stage<KS>& st) {
-  const int sq = tid & 15;
-  const uint32_t cols = M.base.cols;
-  const uint32_t scol = i0 + 8 * (tid >> 4);
-  const bool scol_ok = scol < cols;
-  const uint32_t k = 2 * sq;
-#pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    st.lo[t] = (u32x4){0u, 0u, 0u, 0u};
-    st.hi[t] = st.lo[t];
-    if (scol_ok && k < M.klim[t]) st.lo[t] = ld_at<u32x4>(M.a[t], 2 * (k * cols + scol));
-    if (scol_ok && k + 1 < M.klim[t]) st.hi[t] = ld_at<u32x4>(M.a[t], 2 * ((k + 1) * cols + scol));
-  }
-}
-
-template <int KS, bool FULL>
-__device__ __forceinline__ void pm_issue_f(const PJM<KS>& M, uint32_t g0, int tid, Frag<KS>& f) {
-  const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
-  const uint32_t rows = M.base.rows;
-  const uint32_t r0 = g0 + kStripRows * wave;
-  const uint32_t kk = 8 * lg;
-#pragma unroll
-  for (int t = 0; t < KS; ++t) {
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      const uint32_t ob = r0 + 16 * mb + ln;
-      f.bf[t][mb] = (bf16x8){};
-      if (kk < M.klim[t] && (FULL || ob < rows)) f.bf[t][mb] = ld_at<bf16x8>(M.b[t], 2 * (ob * M.rank[t] + kk));
-    }
-  }
-  const uint32_t rl = r0 + 4 * lg;
-  if (M.base.scale_mode == 2) {
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      const uint32_t rb = rl + 16 * mb;
-      if (FULL || rb + 3 < rows) {
-        const f32x4 q = ld_at<f32x4>(M.base.scales, 4 * rb);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) f.sc[4 * mb + v] = q[v];
-      } else {
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-          f.sc[4 * mb + v] = rb + v < rows ? ld_at<float>(M.base.scales, 4 * (rb + v)) : 1.0f;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int g = 0; g < 8; ++g) f.sc[g] = M.base.tscale;
-  }
-}
-
-template <int KS>
-__device__ __forceinline__ void pm_mfma(const PJM<KS>& M, const Frag<KS>& f, const uint16_t* AT, int ld, int tid,
-                                        Acc<KS>& a) {
-  const int lane = tid & 63, ln = lane & 15, lg = lane >> 4;
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) a.v[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    const int kk = 32 * t + 8 * lg;
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + kk]);
-      a.v[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][0], at, a.v[0][nb], 0, 0, 0);
-      a.v[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][1], at, a.v[1][nb], 0, 0, 0);
-    }
-    if (t + 1 < KS && (M.qmask & (1u << t))) {
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb) a.v[mb][nb] *= M.q[t];
-    }
-  }
-}
-
-template <bool F32OUT, int KS, int FMT, bool FULL>
-__device__ __forceinline__ void pair_units_multi(const PJM<KS>& M, uint16_t* AT, uint32_t i0, uint32_t gA,
-                                                 uint32_t gB, bool hasB, int tid) {
-  constexpr int LD = 32 * KS + 8;
-  Stage<KS> st;
-  pm_issue_a<KS>(M, i0, tid, st);
-  Frag<KS> fa, fb;
-  pm_issue_f<KS, FULL>(M, gA, tid, fa);
-  pp_issue_w<KS, FULL>(M.base, i0, gA, tid, fa);
-  pp_issue_w<KS, FULL>(M.base, i0, hasB ? gB : gA, tid, fb);
-  pp_stage<KS>(st, AT, LD, tid);
-  __syncthreads();
-  {
-    Acc<KS> acc;
-    pm_mfma<KS>(M, fa, AT, LD, tid, acc);
-    pm_issue_f<KS, FULL>(M, hasB ? gB : gA, tid, fb);
-    pp_epilogue<F32OUT, KS, FULL, FMT>(M.base, fa, acc, i0, gA, tid);
-  }
-  asm volatile("" ::: "memory");
-  if (hasB) {
-    Acc<KS> acc;
-    pm_mfma<KS>(M, fb, AT, LD, tid, acc);
-    pp_epilogue<F32OUT, KS, FULL, FMT>(M.base, fb, acc, i0, gB, tid);
-  }
-}
-
-template <bool F32OUT, int KS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_fused_pair_multi(JobTable tab) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
-  const int tid = threadIdx.x;
-  const uint32_t pair = xcd_remap(blockIdx.x, gridDim.x);
-  const PJM<KS> M = pjm_load<KS>(tab, pair);
-  const uint32_t p = pair - M.base.unit_begin;
-  const uint32_t i0 = (p % M.base.bands_n) * kBandCols;
-  const uint32_t gA = (p / M.base.bands_n) * (2 * kWavesPerGroup * kStripRows);
-  const uint32_t gB = gA + kWavesPerGroup * kStripRows;
-  const bool hasB = gB < M.base.rows;
-  const bool full = gB + kWavesPerGroup * kStripRows <= M.base.rows && i0 + kBandCols <= M.base.cols;
-  if (M.base.fmt == 0) {
-    if (full) pair_units_multi<F32OUT, KS, 0, true>(M, AT, i0, gA, gB, hasB, tid);
-    else pair_units_multi<F32OUT, KS, 0, false>(M, AT, i0, gA, gB, hasB, tid);
-  } else {
-    if (full) pair_units_multi<F32OUT, KS, 1, true>(M, AT, i0, gA, gB, hasB, tid);
-    else pair_units_multi<F32OUT, KS, 1, false>(M, AT, i0, gA, gB, hasB, tid);
   }
 }
 
@@ -1088,34 +481,26 @@ hipError_t launch_dequant_tile(const DequantTileArgs& a, int fmt, int scale_mode
 }
 
 template <int KS>
-hipError_t launch_fused_ks(const JobTable& t, bool f32out, bool multi, dim3 grid, size_t lds, hipStream_t stream) {
-  if (multi) {
-    // Two or more LoRAs pad to at least two K-steps.
-    if constexpr (KS >= 2) {
-      if (f32out) hipLaunchKernelGGL((k_fused_pair_multi<true, KS>), grid, dim3(256), lds, stream, t);
-      else hipLaunchKernelGGL((k_fused_pair_multi<false, KS>), grid, dim3(256), lds, stream, t);
-    } else {
-      return hipErrorInvalidValue;
-    }
-  } else {
-    if (f32out) hipLaunchKernelGGL((k_fused_pair<true, KS>), grid, dim3(256), lds, stream, t);
-    else hipLaunchKernelGGL((k_fused_pair<false, KS>), grid, dim3(256), lds, stream, t);
-  }
+hipError_t launch_fused_ks(const JobTable& t, bool f32out, dim3 grid, size_t lds, hipStream_t stream) {
+  if (f32out) hipLaunchKernelGGL((k_fused_pair<true, KS>), grid, dim3(256), lds, stream, t);
+  else hipLaunchKernelGGL((k_fused_pair<false, KS>), grid, dim3(256), lds, stream, t);
   return hipGetLastError();
 }
 
 hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, hipStream_t stream) {
   if (t.total_units == 0) return hipSuccess;
   dim3 grid((unsigned)t.total_units);
+  const int ks = (t.lds_ld - 8) / 32;  // K-steps of the largest job
+  if (multi) return launch_fused_multi(t, f32out, ks, stream);
   size_t lds = (size_t)kBandCols * (size_t)t.lds_ld * sizeof(uint16_t);
-  switch ((t.lds_ld - 8) / 32) {  // K-steps of the largest job
-    case 1: return launch_fused_ks<1>(t, f32out, multi, grid, lds, stream);
-    case 2: return launch_fused_ks<2>(t, f32out, multi, grid, lds, stream);
-    case 3: return launch_fused_ks<3>(t, f32out, multi, grid, lds, stream);
-    case 4: return launch_fused_ks<4>(t, f32out, multi, grid, lds, stream);
-    case 5: return launch_fused_ks<5>(t, f32out, multi, grid, lds, stream);
-    case 6: return launch_fused_ks<6>(t, f32out, multi, grid, lds, stream);
-    case 7: return launch_fused_ks<7>(t, f32out, multi, grid, lds, stream);
+  switch (ks) {
+    case 1: return launch_fused_ks<1>(t, f32out, grid, lds, stream);
+    case 2: return launch_fused_ks<2>(t, f32out, grid, lds, stream);
+    case 3: return launch_fused_ks<3>(t, f32out, grid, lds, stream);
+    case 4: return launch_fused_ks<4>(t, f32out, grid, lds, stream);
+    case 5: return launch_fused_ks<5>(t, f32out, grid, lds, stream);
+    case 6: return launch_fused_ks<6>(t, f32out, grid, lds, stream);
+    case 7: return launch_fused_ks<7>(t, f32out, grid, lds, stream);
     default: return hipErrorInvalidValue;
   }
 }

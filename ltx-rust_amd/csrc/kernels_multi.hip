@@ -1,0 +1,215 @@
+// The several-LoRA fused kernel (k_fused_pair_multi) and its launcher, in a
+// translation unit of its own so that its instantiations compile in parallel
+// with the other kernels. CDNA4 (gfx950, wave64).
+#include "kernels_dev.h"
+
+namespace ltxw {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Several LoRAs per tensor, two units per workgroup. The LoRAs sit side by
+// side along K (each padded to 32) and the host describes every K-step
+// (StepDev: the step's A rows, B columns, rank and present ranks). One
+// accumulator set carries the whole delta: at the last step of LoRA l, with
+// LoRA l+1 following, the accumulator is multiplied by q = c_l / c_{l+1}, and
+// the epilogue multiplies by the last coefficient:
+//   delta = c_last (... ((B_0 A_0) q_0 + B_1 A_1) q_1 ...) = sum_l c_l B_l A_l
+// up to a few f32 roundings (the host routes coefficients whose ratios could
+// overflow or underflow to the reference-order kernel).
+// ---------------------------------------------------------------------------
+template <int KS>
+struct PJM {
+  PJ base;  // coeff / cmul: the last LoRA's coefficient
+  const uint16_t* a[KS];
+  const uint16_t* b[KS];
+  uint32_t rank[KS];
+  uint32_t klim[KS];
+  float q[KS];
+  uint32_t qmask;
+};
+
+template <int KS>
+__device__ __forceinline__ PJM<KS> pjm_load(const JobTable& t, uint64_t unit) {
+  JobDev J;
+  load_job(t, unit, J);
+  PJM<KS> m;
+  m.base.w = uni_ptr(J.w);
+  m.base.out = uni_ptr(J.out);
+  m.base.scales = uni_ptr(J.scales);
+  m.base.a = nullptr;
+  m.base.b = nullptr;
+  m.base.rows = uni((uint32_t)J.rows);
+  m.base.cols = uni((uint32_t)J.cols);
+  m.base.rank = 0;
+  m.base.bands_n = uni((uint32_t)J.bands_n);
+  m.base.scale_mode = uni((uint32_t)J.scale_mode);
+  m.base.fmt = uni((uint32_t)J.fmt);
+  m.base.tscale = m.base.scale_mode == 1 ? *G(uni_ptr(J.scales)) : 1.0f;
+  m.base.coeff = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.coeff_out)));
+  m.base.cmul = uni(J.cmul);
+  m.base.unit_begin = uni((uint32_t)J.unit_begin);
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    m.a[s] = uni_ptr(J.step[s].a);
+    m.b[s] = uni_ptr(J.step[s].b);
+    m.rank[s] = uni(J.step[s].rank);
+    m.klim[s] = uni(J.step[s].klim);
+    m.q[s] = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.step[s].q)));
+  }
+  m.qmask = uni(J.qmask);
+  return m;
+}
+
+template <int KS>
+__device__ __forceinline__ void pm_issue_a(const PJM<KS>& M, uint32_t i0, int tid, Stage<KS>& st) {
+  const int sq = tid & 15;
+  const uint32_t cols = M.base.cols;
+  const uint32_t scol = i0 + 8 * (tid >> 4);
+  const bool scol_ok = scol < cols;
+  const uint32_t k = 2 * sq;
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    st.lo[t] = (u32x4){0u, 0u, 0u, 0u};
+    st.hi[t] = st.lo[t];
+    if (scol_ok && k < M.klim[t]) st.lo[t] = ld_at<u32x4>(M.a[t], 2 * (k * cols + scol));
+    if (scol_ok && k + 1 < M.klim[t]) st.hi[t] = ld_at<u32x4>(M.a[t], 2 * ((k + 1) * cols + scol));
+  }
+}
+
+template <int KS, bool FULL>
+__device__ __forceinline__ void pm_issue_f(const PJM<KS>& M, uint32_t g0, int tid, Frag<KS>& f) {
+  const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
+  const uint32_t rows = M.base.rows;
+  const uint32_t r0 = g0 + kStripRows * wave;
+  const uint32_t kk = 8 * lg;
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const uint32_t ob = r0 + 16 * mb + ln;
+      f.bf[t][mb] = (bf16x8){};
+      if (kk < M.klim[t] && (FULL || ob < rows)) f.bf[t][mb] = ld_at<bf16x8>(M.b[t], 2 * (ob * M.rank[t] + kk));
+    }
+  }
+  const uint32_t rl = r0 + 4 * lg;
+  if (M.base.scale_mode == 2) {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const uint32_t rb = rl + 16 * mb;
+      if (FULL || rb + 3 < rows) {
+        const f32x4 q = ld_at<f32x4>(M.base.scales, 4 * rb);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) f.sc[4 * mb + v] = q[v];
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          f.sc[4 * mb + v] = rb + v < rows ? ld_at<float>(M.base.scales, 4 * (rb + v)) : 1.0f;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < 8; ++g) f.sc[g] = M.base.tscale;
+  }
+}
+
+template <int KS>
+__device__ __forceinline__ void pm_mfma(const PJM<KS>& M, const Frag<KS>& f, const uint16_t* AT, int ld, int tid,
+                                        Acc<KS>& a) {
+  const int lane = tid & 63, ln = lane & 15, lg = lane >> 4;
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) a.v[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    const int kk = 32 * t + 8 * lg;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+      const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + kk]);
+      a.v[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][0], at, a.v[0][nb], 0, 0, 0);
+      a.v[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][1], at, a.v[1][nb], 0, 0, 0);
+    }
+    if (t + 1 < KS && (M.qmask & (1u << t))) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) a.v[mb][nb] *= M.q[t];
+    }
+  }
+}
+
+template <bool F32OUT, int KS, int FMT, bool FULL>
+__device__ __forceinline__ void pair_units_multi(const PJM<KS>& M, uint16_t* AT, uint32_t i0, uint32_t gA,
+                                                 uint32_t gB, bool hasB, int tid) {
+  constexpr int LD = 32 * KS + 8;
+  Stage<KS> st;
+  pm_issue_a<KS>(M, i0, tid, st);
+  Frag<KS> fa, fb;
+  pm_issue_f<KS, FULL>(M, gA, tid, fa);
+  pp_issue_w<KS, FULL>(M.base, i0, gA, tid, fa);
+  pp_issue_w<KS, FULL>(M.base, i0, hasB ? gB : gA, tid, fb);
+  pp_stage<KS>(st, AT, LD, tid);
+  __syncthreads();
+  {
+    Acc<KS> acc;
+    pm_mfma<KS>(M, fa, AT, LD, tid, acc);
+    pm_issue_f<KS, FULL>(M, hasB ? gB : gA, tid, fb);
+    pp_epilogue<F32OUT, KS, FULL, FMT>(M.base, fa, acc, i0, gA, tid);
+  }
+  asm volatile("" ::: "memory");
+  if (hasB) {
+    Acc<KS> acc;
+    pm_mfma<KS>(M, fb, AT, LD, tid, acc);
+    pp_epilogue<F32OUT, KS, FULL, FMT>(M.base, fb, acc, i0, gB, tid);
+  }
+}
+
+template <bool F32OUT, int KS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_fused_pair_multi(JobTable tab) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
+  const int tid = threadIdx.x;
+  const uint32_t pair = xcd_remap(blockIdx.x, gridDim.x);
+  const PJM<KS> M = pjm_load<KS>(tab, pair);
+  const uint32_t p = pair - M.base.unit_begin;
+  const uint32_t i0 = (p % M.base.bands_n) * kBandCols;
+  const uint32_t gA = (p / M.base.bands_n) * (2 * kWavesPerGroup * kStripRows);
+  const uint32_t gB = gA + kWavesPerGroup * kStripRows;
+  const bool hasB = gB < M.base.rows;
+  const bool full = gB + kWavesPerGroup * kStripRows <= M.base.rows && i0 + kBandCols <= M.base.cols;
+  if (M.base.fmt == 0) {
+    if (full) pair_units_multi<F32OUT, KS, 0, true>(M, AT, i0, gA, gB, hasB, tid);
+    else pair_units_multi<F32OUT, KS, 0, false>(M, AT, i0, gA, gB, hasB, tid);
+  } else {
+    if (full) pair_units_multi<F32OUT, KS, 1, true>(M, AT, i0, gA, gB, hasB, tid);
+    else pair_units_multi<F32OUT, KS, 1, false>(M, AT, i0, gA, gB, hasB, tid);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_fused_multi(const JobTable& t, bool f32out, int ks, hipStream_t stream) {
+  if (t.total_units == 0) return hipSuccess;
+  dim3 grid((unsigned)t.total_units);
+  size_t lds = (size_t)kBandCols * (size_t)t.lds_ld * sizeof(uint16_t);
+#define LTXW_MULTI_LAUNCH(KS)                                                                  \
+  case KS:                                                                                     \
+    if (f32out) hipLaunchKernelGGL((k_fused_pair_multi<true, KS>), grid, dim3(256), lds, stream, t); \
+    else hipLaunchKernelGGL((k_fused_pair_multi<false, KS>), grid, dim3(256), lds, stream, t);       \
+    break;
+  // Two or more LoRAs pad to at least two K-steps; one LoRA may take this
+  // kernel too (any K-steps).
+  switch (ks) {
+    LTXW_MULTI_LAUNCH(1)
+    LTXW_MULTI_LAUNCH(2)
+    LTXW_MULTI_LAUNCH(3)
+    LTXW_MULTI_LAUNCH(4)
+    LTXW_MULTI_LAUNCH(5)
+    LTXW_MULTI_LAUNCH(6)
+    LTXW_MULTI_LAUNCH(7)
+    default: return hipErrorInvalidValue;
+  }
+#undef LTXW_MULTI_LAUNCH
+  return hipGetLastError();
+}
+
+}  // namespace ltxw
