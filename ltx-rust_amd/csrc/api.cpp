@@ -171,8 +171,14 @@ bool fused_ok(const ltxw_tensor_desc& d) {
   int k = 0;
   for (int l = 0; l < d.n_loras; ++l) {
     const uint64_t r = (uint64_t)d.loras[l].rank;
-    if (d.loras[l].dtype != LTXW_FACTOR_BF16) return false;
-    if (r % 8 != 0 || !aligned(d.loras[l].a, 16) || !aligned(d.loras[l].b, 16)) return false;
+    // bf16, f16 and FP8 factors, the same type for all of a tensor's LoRAs
+    // (one compiled factor type per launch); f32 factors keep the reference
+    // order.
+    const int dt = d.loras[l].dtype;
+    if (dt == LTXW_FACTOR_F32 || dt != d.loras[0].dtype) return false;
+    // 8 consecutive elements per load: 16 bytes (16-bit types) or 8 (FP8).
+    const size_t vec = 8 * (size_t)factor_bytes(dt);
+    if (r % 8 != 0 || !aligned(d.loras[l].a, vec) || !aligned(d.loras[l].b, vec)) return false;
     if (2 * r * (uint64_t)d.rows > lim || 2 * r * (uint64_t)d.cols > lim) return false;
     // Several LoRAs share one accumulator, rescaled by c_l / c_{l+1} between
     // them: keep those ratios and the rescaled partial sums far from f32
@@ -191,10 +197,11 @@ void plan_fused(ltxw::JobDev& j) {
   for (int l = 0; l < j.n_loras; ++l) {
     const ltxw::LoraDev& L = j.lora[l];
     const int nks = ltxw::pad_rank(L.rank) / 32;
+    const size_t esz = (size_t)factor_bytes(L.dtype);
     for (int kt = 0; kt < nks && t < ltxw::kMaxSteps; ++kt, ++t) {
       ltxw::StepDev& s = j.step[t];
-      s.a = L.a + (size_t)32 * kt * (size_t)j.cols;
-      s.b = L.b + 32 * kt;
+      s.a = (const char*)L.a + esz * 32 * kt * (size_t)j.cols;
+      s.b = (const char*)L.b + esz * 32 * kt;
       s.rank = (uint32_t)L.rank;
       s.klim = (uint32_t)(L.rank - 32 * kt);
       s.q = 1.0f;
@@ -292,9 +299,10 @@ int job_k(const ltxw::JobDev& j) {
   return k;
 }
 
-// One fused launch over `jobs` (all fused_ok, same out dtype, multi flag and
-// K-steps): one workgroup per 128-column band and 256 rows of every job.
-int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool multi) {
+// One fused launch over `jobs` (all fused_ok, same out dtype, kernel, factor
+// type and K-steps): one workgroup per 128-column band and 256 rows of every
+// job.
+int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool multi, int fdt) {
   if (jobs.empty()) return LTXW_OK;
   int kmax = 0;
   for (auto& j : jobs) kmax = std::max(kmax, job_k(j));
@@ -328,7 +336,7 @@ int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool 
     t.jobs = reinterpret_cast<const ltxw::JobDev*>(slot->dev);
     t.begins = reinterpret_cast<const int64_t*>((char*)slot->dev + off_b);
   }
-  HIP_TRY(ctx, ltxw::launch_fused(t, f32out, multi, ctx->compute), "fused kernel launch");
+  HIP_TRY(ctx, ltxw::launch_fused(t, f32out, multi, fdt, ctx->compute), "fused kernel launch");
   return LTXW_OK;
 }
 
@@ -341,10 +349,12 @@ int ltxw::run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n, const D
     int rc = check_desc(ctx, descs[k], &counts[(size_t)k]);
     if (rc) return rc;
   }
-  // Fused launches are bucketed by (f32 out, multi-LoRA, K-steps), so that the
-  // register arrays of each launch are sized for its own jobs' rank, not for
-  // the largest rank of the call.
-  std::map<std::tuple<int, int, int>, std::vector<ltxw::JobDev>> buckets;
+  // Fused launches are bucketed by (f32 out, kernel, K-steps, factor type),
+  // so that the register arrays of each launch are sized for its own jobs'
+  // rank, not for the largest rank of the call. One bf16 LoRA takes the
+  // single-LoRA kernel; several LoRAs or other factor types the several-LoRA
+  // one.
+  std::map<std::tuple<int, int, int, int>, std::vector<ltxw::JobDev>> buckets;
   for (int k = 0; k < n; ++k) {
     const ltxw_tensor_desc& d = descs[k];
     uint64_t cnt = counts[(size_t)k];
@@ -357,12 +367,14 @@ int ltxw::run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n, const D
       rc = ltxw::format_bytes(d.fmt) == 1 ? run_dequant(ctx, d, cnt) : run_generic(ctx, d, 0, cnt);
     } else {
       ltxw::JobDev j = to_job(d);
-      buckets[{d.out_dtype == LTXW_OUT_F32, d.n_loras > 1, job_k(j) / 32}].push_back(j);
+      const int fdt = d.loras[0].dtype;
+      const bool multi = d.n_loras > 1 || fdt != LTXW_FACTOR_BF16;
+      buckets[{d.out_dtype == LTXW_OUT_F32, multi, job_k(j) / 32, fdt}].push_back(j);
     }
     if (rc) return rc;
   }
   for (auto& kv : buckets) {
-    int rc = run_fused(ctx, kv.second, std::get<0>(kv.first) == 1, std::get<1>(kv.first) == 1);
+    int rc = run_fused(ctx, kv.second, std::get<0>(kv.first) == 1, std::get<1>(kv.first) == 1, std::get<3>(kv.first));
     if (rc) return rc;
   }
   return LTXW_OK;

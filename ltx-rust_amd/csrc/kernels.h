@@ -31,8 +31,8 @@ struct LoraDev {
 // host: the LoRAs of a tensor sit side by side along K, each padded to 32,
 // and LoRA l owns the steps [kst_l, kst_l + pad_rank(rank_l) / 32).
 struct StepDev {
-  const uint16_t* a;  // A of the step's LoRA + 32 kt rows (row stride cols)
-  const uint16_t* b;  // B of the step's LoRA + 32 kt columns (row stride rank)
+  const void* a;      // A of the step's LoRA + 32 kt rows (row stride cols)
+  const void* b;      // B of the step's LoRA + 32 kt columns (row stride rank)
   uint32_t rank;      // the LoRA's rank
   uint32_t klim;      // ranks of the step that exist: rank - 32 kt (>= 32: all)
   float q;            // factor applied to the accumulator after the step
@@ -133,13 +133,21 @@ hipError_t launch_dequant_tile(const DequantTileArgs& a, int fmt, int scale_mode
 // total padded rank <= kRankMax, the same K-steps for every job
 // (lds_ld == 8 + 32 * K-steps). One workgroup per pair of vertically
 // adjacent 128-row units (kPairRows rows); unit_begin and total_units count
-// pairs. `multi`: several LoRAs per tensor. Every job's qmask, cmul,
-// coeff_out and step[] are filled (plan_fused in api.cpp).
-hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, hipStream_t stream);
+// pairs. `multi`: the several-LoRA kernel (several LoRAs per tensor, or
+// factors other than bf16), whose jobs all have factors of element type
+// `fdt`. Every job's qmask, cmul, coeff_out and step[] are filled
+// (plan_fused in api.cpp).
+hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, int fdt, hipStream_t stream);
 
-// The several-LoRA kernel alone (kernels_multi.hip); `ks` K-steps (1-7).
-// launch_fused calls it for `multi`.
-hipError_t launch_fused_multi(const JobTable& t, bool f32out, int ks, hipStream_t stream);
+// The several-LoRA kernel alone (kernels_multi_dev.h); `ks` K-steps (1-7),
+// every job's factors of element type `fdt` (ltxw_factor_dtype: 0 bf16,
+// 2 f16, 3 e4m3fn, 4 e5m2). launch_fused calls it for `multi`.
+hipError_t launch_fused_multi(const JobTable& t, bool f32out, int ks, int fdt, hipStream_t stream);
+// Its instantiations, one translation unit per factor type (kernels_multi_*.hip).
+hipError_t launch_fused_multi_bf16(const JobTable& t, bool f32out, int ks, hipStream_t stream);
+hipError_t launch_fused_multi_f16(const JobTable& t, bool f32out, int ks, hipStream_t stream);
+hipError_t launch_fused_multi_e4m3fn(const JobTable& t, bool f32out, int ks, hipStream_t stream);
+hipError_t launch_fused_multi_e5m2(const JobTable& t, bool f32out, int ks, hipStream_t stream);
 
 // Rows of one workgroup of the single-LoRA kernel.
 constexpr int kPairRows = 2 * kWavesPerGroup * kStripRows;

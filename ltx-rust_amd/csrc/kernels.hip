@@ -487,11 +487,11 @@ hipError_t launch_fused_ks(const JobTable& t, bool f32out, dim3 grid, size_t lds
   return hipGetLastError();
 }
 
-hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, hipStream_t stream) {
+hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, int fdt, hipStream_t stream) {
   if (t.total_units == 0) return hipSuccess;
   dim3 grid((unsigned)t.total_units);
   const int ks = (t.lds_ld - 8) / 32;  // K-steps of the largest job
-  if (multi) return launch_fused_multi(t, f32out, ks, stream);
+  if (multi) return launch_fused_multi(t, f32out, ks, fdt, stream);
   size_t lds = (size_t)kBandCols * (size_t)t.lds_ld * sizeof(uint16_t);
   switch (ks) {
     case 1: return launch_fused_ks<1>(t, f32out, grid, lds, stream);
@@ -501,6 +501,16 @@ hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, hipStream_t 
     case 5: return launch_fused_ks<5>(t, f32out, grid, lds, stream);
     case 6: return launch_fused_ks<6>(t, f32out, grid, lds, stream);
     case 7: return launch_fused_ks<7>(t, f32out, grid, lds, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_fused_multi(const JobTable& t, bool f32out, int ks, int fdt, hipStream_t stream) {
+  switch (fdt) {
+    case 0: return launch_fused_multi_bf16(t, f32out, ks, stream);
+    case 2: return launch_fused_multi_f16(t, f32out, ks, stream);
+    case 3: return launch_fused_multi_e4m3fn(t, f32out, ks, stream);
+    case 4: return launch_fused_multi_e5m2(t, f32out, ks, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -317,8 +317,9 @@ __device__ __forceinline__ void pp_issue_f(const PJ& J, uint32_t i0, uint32_t g0
   }
 }
 
-template <int KS, bool FULL>
-__device__ __forceinline__ void pp_issue_w(const PJ& J, uint32_t i0, uint32_t g0, int tid, Frag<KS>& f) {
+// (FragT: any fragment set with the wv[8] / sc[8] members.)
+template <int KS, bool FULL, class FragT>
+__device__ __forceinline__ void pp_issue_w(const PJ& J, uint32_t i0, uint32_t g0, int tid, FragT& f) {
   const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
   const uint32_t rows = J.rows, cols = J.cols;
   const uint32_t r0 = g0 + kStripRows * wave;
@@ -371,8 +372,8 @@ __device__ __forceinline__ void pp_mfma(const Frag<KS>& f, const uint16_t* AT, i
   }
 }
 
-template <bool F32OUT, int KS, bool FULL, int FMT>
-__device__ __forceinline__ void pp_epilogue(const PJ& J, const Frag<KS>& f, Acc<KS>& a, uint32_t i0, uint32_t g0,
+template <bool F32OUT, int KS, bool FULL, int FMT, class FragT>
+__device__ __forceinline__ void pp_epilogue(const PJ& J, const FragT& f, Acc<KS>& a, uint32_t i0, uint32_t g0,
                                             int tid) {
   const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
   const uint32_t rows = J.rows, cols = J.cols;

@@ -1,6 +1,8 @@
-// The several-LoRA fused kernel (k_fused_pair_multi) and its launcher, in a
-// translation unit of its own so that its instantiations compile in parallel
-// with the other kernels. CDNA4 (gfx950, wave64).
+// The several-LoRA fused kernel (k_fused_pair_multi), templated on the factor
+// element type; kernels_multi_*.hip instantiate it, one factor type per
+// translation unit, so that they compile in parallel. CDNA4 (gfx950, wave64).
+#pragma once
+
 #include "kernels_dev.h"
 
 namespace ltxw {
@@ -17,11 +19,54 @@ namespace {
 // up to a few f32 roundings (the host routes coefficients whose ratios could
 // overflow or underflow to the reference-order kernel).
 // ---------------------------------------------------------------------------
+// Factor element types the kernel takes (ltxw_factor_dtype): bf16 (0) and
+// f16 (2) feed the bf16 / f16 MFMA as stored; e4m3fn (3) and e5m2 (4) are
+// widened to bf16 in registers, which is exact (every FP8 value, NaN and Inf
+// included, is a bf16 value), so their products are the same as the
+// reference's f32 ones. F32 factors take the reference-order kernel.
+template <int FDT>
+struct FactorRaw {
+  using T = u32x4;  // 8 elements of 16 bits
+  static constexpr uint32_t kBytes = 2;
+};
+template <>
+struct FactorRaw<3> {
+  using T = u32x2;  // 8 FP8 bytes
+  static constexpr uint32_t kBytes = 1;
+};
+template <>
+struct FactorRaw<4> : FactorRaw<3> {};
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// 8 raw elements -> 8 MFMA input elements, as 4 packed pairs.
+template <int FDT>
+__device__ __forceinline__ u32x4 to_pairs(const typename FactorRaw<FDT>::T& r) {
+  if constexpr (FDT == 3 || FDT == 4) {
+    float v[8];
+    decode4(r[0], FDT - 3, v);
+    decode4(r[1], FDT - 3, v + 4);
+    return (u32x4){pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7])};
+  } else {
+    return r;
+  }
+}
+
+template <int FDT>
+__device__ __forceinline__ f32x4 mfma_step(const u32x4& a, const u32x4& b, const f32x4& c) {
+  if constexpr (FDT == 2)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
 template <int KS>
 struct PJM {
   PJ base;  // coeff / cmul: the last LoRA's coefficient
-  const uint16_t* a[KS];
-  const uint16_t* b[KS];
+  const void* a[KS];
+  const void* b[KS];
   uint32_t rank[KS];
   uint32_t klim[KS];
   float q[KS];
@@ -60,8 +105,22 @@ __device__ __forceinline__ PJM<KS> pjm_load(const JobTable& t, uint64_t unit) {
   return m;
 }
 
-template <int KS>
-__device__ __forceinline__ void pm_issue_a(const PJM<KS>& M, uint32_t i0, int tid, Stage<KS>& st) {
+template <int KS, int FDT>
+struct StageM {
+  typename FactorRaw<FDT>::T lo[KS], hi[KS];
+};
+
+template <int KS, int FDT>
+struct FragM {
+  typename FactorRaw<FDT>::T bf[KS][2];
+  u32x2 wv[8];
+  float sc[8];
+};
+
+template <int KS, int FDT>
+__device__ __forceinline__ void pm_issue_a(const PJM<KS>& M, uint32_t i0, int tid, StageM<KS, FDT>& st) {
+  using R = typename FactorRaw<FDT>::T;
+  constexpr uint32_t E = FactorRaw<FDT>::kBytes;
   const int sq = tid & 15;
   const uint32_t cols = M.base.cols;
   const uint32_t scol = i0 + 8 * (tid >> 4);
@@ -69,15 +128,32 @@ __device__ __forceinline__ void pm_issue_a(const PJM<KS>& M, uint32_t i0, int ti
   const uint32_t k = 2 * sq;
 #pragma unroll
   for (int t = 0; t < KS; ++t) {
-    st.lo[t] = (u32x4){0u, 0u, 0u, 0u};
-    st.hi[t] = st.lo[t];
-    if (scol_ok && k < M.klim[t]) st.lo[t] = ld_at<u32x4>(M.a[t], 2 * (k * cols + scol));
-    if (scol_ok && k + 1 < M.klim[t]) st.hi[t] = ld_at<u32x4>(M.a[t], 2 * ((k + 1) * cols + scol));
+    st.lo[t] = R{};
+    st.hi[t] = R{};
+    if (scol_ok && k < M.klim[t]) st.lo[t] = ld_at<R>(M.a[t], E * (k * cols + scol));
+    if (scol_ok && k + 1 < M.klim[t]) st.hi[t] = ld_at<R>(M.a[t], E * ((k + 1) * cols + scol));
   }
 }
 
-template <int KS, bool FULL>
-__device__ __forceinline__ void pm_issue_f(const PJM<KS>& M, uint32_t g0, int tid, Frag<KS>& f) {
+// As pp_stage, from raw factor elements.
+template <int KS, int FDT>
+__device__ __forceinline__ void pm_stage(const StageM<KS, FDT>& st, uint16_t* AT, int ld, int tid) {
+  const int sq = tid & 15;
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    const u32x4 lo = to_pairs<FDT>(st.lo[t]), hi = to_pairs<FDT>(st.hi[t]);
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const uint32_t pair = __builtin_amdgcn_perm(hi[jj >> 1], lo[jj >> 1], (jj & 1) ? 0x07060302u : 0x05040100u);
+      *reinterpret_cast<uint32_t*>(&AT[(jj * 16 + (tid >> 4)) * ld + 32 * t + 2 * sq]) = pair;
+    }
+  }
+}
+
+template <int KS, bool FULL, int FDT>
+__device__ __forceinline__ void pm_issue_f(const PJM<KS>& M, uint32_t g0, int tid, FragM<KS, FDT>& f) {
+  using R = typename FactorRaw<FDT>::T;
+  constexpr uint32_t E = FactorRaw<FDT>::kBytes;
   const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
   const uint32_t rows = M.base.rows;
   const uint32_t r0 = g0 + kStripRows * wave;
@@ -87,8 +163,8 @@ __device__ __forceinline__ void pm_issue_f(const PJM<KS>& M, uint32_t g0, int ti
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       const uint32_t ob = r0 + 16 * mb + ln;
-      f.bf[t][mb] = (bf16x8){};
-      if (kk < M.klim[t] && (FULL || ob < rows)) f.bf[t][mb] = ld_at<bf16x8>(M.b[t], 2 * (ob * M.rank[t] + kk));
+      f.bf[t][mb] = R{};
+      if (kk < M.klim[t] && (FULL || ob < rows)) f.bf[t][mb] = ld_at<R>(M.b[t], E * (ob * M.rank[t] + kk));
     }
   }
   const uint32_t rl = r0 + 4 * lg;
@@ -112,8 +188,8 @@ __device__ __forceinline__ void pm_issue_f(const PJM<KS>& M, uint32_t g0, int ti
   }
 }
 
-template <int KS>
-__device__ __forceinline__ void pm_mfma(const PJM<KS>& M, const Frag<KS>& f, const uint16_t* AT, int ld, int tid,
+template <int KS, int FDT>
+__device__ __forceinline__ void pm_mfma(const PJM<KS>& M, const FragM<KS, FDT>& f, const uint16_t* AT, int ld, int tid,
                                         Acc<KS>& a) {
   const int lane = tid & 63, ln = lane & 15, lg = lane >> 4;
 #pragma unroll
@@ -123,11 +199,12 @@ __device__ __forceinline__ void pm_mfma(const PJM<KS>& M, const Frag<KS>& f, con
 #pragma unroll
   for (int t = 0; t < KS; ++t) {
     const int kk = 32 * t + 8 * lg;
+    const u32x4 b0 = to_pairs<FDT>(f.bf[t][0]), b1 = to_pairs<FDT>(f.bf[t][1]);
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) {
-      const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + kk]);
-      a.v[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][0], at, a.v[0][nb], 0, 0, 0);
-      a.v[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][1], at, a.v[1][nb], 0, 0, 0);
+      const u32x4 at = *reinterpret_cast<const u32x4*>(&AT[(nb * 16 + ln) * ld + kk]);
+      a.v[0][nb] = mfma_step<FDT>(b0, at, a.v[0][nb]);
+      a.v[1][nb] = mfma_step<FDT>(b1, at, a.v[1][nb]);
     }
     if (t + 1 < KS && (M.qmask & (1u << t))) {
 #pragma unroll
@@ -138,33 +215,33 @@ __device__ __forceinline__ void pm_mfma(const PJM<KS>& M, const Frag<KS>& f, con
   }
 }
 
-template <bool F32OUT, int KS, int FMT, bool FULL>
+template <bool F32OUT, int KS, int FMT, bool FULL, int FDT>
 __device__ __forceinline__ void pair_units_multi(const PJM<KS>& M, uint16_t* AT, uint32_t i0, uint32_t gA,
                                                  uint32_t gB, bool hasB, int tid) {
   constexpr int LD = 32 * KS + 8;
-  Stage<KS> st;
-  pm_issue_a<KS>(M, i0, tid, st);
-  Frag<KS> fa, fb;
-  pm_issue_f<KS, FULL>(M, gA, tid, fa);
+  StageM<KS, FDT> st;
+  pm_issue_a<KS, FDT>(M, i0, tid, st);
+  FragM<KS, FDT> fa, fb;
+  pm_issue_f<KS, FULL, FDT>(M, gA, tid, fa);
   pp_issue_w<KS, FULL>(M.base, i0, gA, tid, fa);
   pp_issue_w<KS, FULL>(M.base, i0, hasB ? gB : gA, tid, fb);
-  pp_stage<KS>(st, AT, LD, tid);
+  pm_stage<KS, FDT>(st, AT, LD, tid);
   __syncthreads();
   {
     Acc<KS> acc;
-    pm_mfma<KS>(M, fa, AT, LD, tid, acc);
-    pm_issue_f<KS, FULL>(M, hasB ? gB : gA, tid, fb);
+    pm_mfma<KS, FDT>(M, fa, AT, LD, tid, acc);
+    pm_issue_f<KS, FULL, FDT>(M, hasB ? gB : gA, tid, fb);
     pp_epilogue<F32OUT, KS, FULL, FMT>(M.base, fa, acc, i0, gA, tid);
   }
   asm volatile("" ::: "memory");
   if (hasB) {
     Acc<KS> acc;
-    pm_mfma<KS>(M, fb, AT, LD, tid, acc);
+    pm_mfma<KS, FDT>(M, fb, AT, LD, tid, acc);
     pp_epilogue<F32OUT, KS, FULL, FMT>(M.base, fb, acc, i0, gB, tid);
   }
 }
 
-template <bool F32OUT, int KS>
+template <bool F32OUT, int KS, int FDT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_fused_pair_multi(JobTable tab) {
   extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
   const int tid = threadIdx.x;
@@ -177,27 +254,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   const bool hasB = gB < M.base.rows;
   const bool full = gB + kWavesPerGroup * kStripRows <= M.base.rows && i0 + kBandCols <= M.base.cols;
   if (M.base.fmt == 0) {
-    if (full) pair_units_multi<F32OUT, KS, 0, true>(M, AT, i0, gA, gB, hasB, tid);
-    else pair_units_multi<F32OUT, KS, 0, false>(M, AT, i0, gA, gB, hasB, tid);
+    if (full) pair_units_multi<F32OUT, KS, 0, true, FDT>(M, AT, i0, gA, gB, hasB, tid);
+    else pair_units_multi<F32OUT, KS, 0, false, FDT>(M, AT, i0, gA, gB, hasB, tid);
   } else {
-    if (full) pair_units_multi<F32OUT, KS, 1, true>(M, AT, i0, gA, gB, hasB, tid);
-    else pair_units_multi<F32OUT, KS, 1, false>(M, AT, i0, gA, gB, hasB, tid);
+    if (full) pair_units_multi<F32OUT, KS, 1, true, FDT>(M, AT, i0, gA, gB, hasB, tid);
+    else pair_units_multi<F32OUT, KS, 1, false, FDT>(M, AT, i0, gA, gB, hasB, tid);
   }
 }
 
-}  // namespace
-
-hipError_t launch_fused_multi(const JobTable& t, bool f32out, int ks, hipStream_t stream) {
+template <int FDT>
+hipError_t launch_multi_fdt(const JobTable& t, bool f32out, int ks, hipStream_t stream) {
   if (t.total_units == 0) return hipSuccess;
   dim3 grid((unsigned)t.total_units);
   size_t lds = (size_t)kBandCols * (size_t)t.lds_ld * sizeof(uint16_t);
-#define LTXW_MULTI_LAUNCH(KS)                                                                  \
-  case KS:                                                                                     \
-    if (f32out) hipLaunchKernelGGL((k_fused_pair_multi<true, KS>), grid, dim3(256), lds, stream, t); \
-    else hipLaunchKernelGGL((k_fused_pair_multi<false, KS>), grid, dim3(256), lds, stream, t);       \
+#define LTXW_MULTI_LAUNCH(KS)                                                                            \
+  case KS:                                                                                               \
+    if (f32out) hipLaunchKernelGGL((k_fused_pair_multi<true, KS, FDT>), grid, dim3(256), lds, stream, t); \
+    else hipLaunchKernelGGL((k_fused_pair_multi<false, KS, FDT>), grid, dim3(256), lds, stream, t);       \
     break;
-  // Two or more LoRAs pad to at least two K-steps; one LoRA may take this
-  // kernel too (any K-steps).
   switch (ks) {
     LTXW_MULTI_LAUNCH(1)
     LTXW_MULTI_LAUNCH(2)
@@ -211,5 +285,7 @@ hipError_t launch_fused_multi(const JobTable& t, bool f32out, int ks, hipStream_
 #undef LTXW_MULTI_LAUNCH
   return hipGetLastError();
 }
+
+}  // namespace
 
 }  // namespace ltxw

@@ -6,6 +6,14 @@ import ltx_weights as lw
 import oracle_lib as O
 
 FMT_TO_ORC = {lw.FMT_E4M3FN: O.E4M3FN, lw.FMT_E5M2: O.E5M2}
+# LoRA factor element types (a case's LoRA tuples are (B, A, rank, coeff) or
+# (B, A, rank, coeff, factor type); bf16 when absent).
+FDT_TO_ORC = {lw.FACTOR_BF16: O.BF16, lw.FACTOR_F32: O.F32, lw.FACTOR_F16: O.F16,
+              lw.FACTOR_E4M3FN: O.E4M3FN, lw.FACTOR_E5M2: O.E5M2}
+
+
+def lora_fdt(lo):
+    return lo[4] if len(lo) > 4 else lw.FACTOR_BF16
 
 
 class Dev:
@@ -22,8 +30,9 @@ class Dev:
         self.w = self.w_base + w_offset
         self.s = self._put(case["scales"]) if case["scales"] is not None else None
         self.loras = []
-        for b, a, rank, coeff in case["loras"]:
-            self.loras.append((self._put(b), self._put(a), rank, coeff))
+        for lo in case["loras"]:
+            b, a, rank, coeff = lo[:4]
+            self.loras.append((self._put(b), self._put(a), rank, coeff, lora_fdt(lo)))
         ob = 4 if out_dtype == lw.OUT_F32 else 2
         self.out_base = ctx.alloc(max(1, n * ob + out_offset + 64))
         self.ptrs.append(self.out_base)
@@ -64,7 +73,7 @@ def oracle_args(case, row_sel=None):
     """Oracle inputs, optionally restricted to a subset of output rows (rows
     are independent: row o needs W[o], scale[o] and B[o] only)."""
     w, s = case["w"], case["scales"]
-    loras = [(b, a, O.BF16, coeff) for (b, a, rank, coeff) in case["loras"]]
+    loras = [(lo[0], lo[1], FDT_TO_ORC[lora_fdt(lo)], lo[3]) for lo in case["loras"]]
     if row_sel is not None:
         w = w[row_sel]
         if s is not None and case["scale_mode"] == lw.SCALE_ROW:

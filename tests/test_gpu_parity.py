@@ -134,6 +134,37 @@ def test_several_loras_extreme_coefficients_use_reference_order(ctx, coeffs):
     assert np.array_equal(got.view(np.uint16), U.oracle_bf16(case).view(np.uint16))
 
 
+def factor_codes(rng, fdt, shape):
+    """Factor elements of type fdt with magnitudes below 1/8: f16 from
+    N(0, 0.02^2); FP8 codes with small exponent fields, both signs, zeros and
+    subnormals included."""
+    if fdt == lw.FACTOR_F16:
+        return rng.normal(0.0, 0.02, size=shape).astype(np.float16).view(np.uint16)
+    exp_bits, man_bits, e_max = (4, 3, 4) if fdt == lw.FACTOR_E4M3FN else (5, 2, 12)
+    e = rng.integers(0, e_max + 1, size=shape)
+    m = rng.integers(0, 1 << man_bits, size=shape)
+    sgn = rng.integers(0, 2, size=shape)
+    return ((sgn << 7) | (e << man_bits) | m).astype(np.uint8)
+
+
+@pytest.mark.parametrize("fdt", [lw.FACTOR_F16, lw.FACTOR_E4M3FN, lw.FACTOR_E5M2])
+@pytest.mark.parametrize("ranks,shape", [(((64, 1.0),), (300, 520)), (((32, 1.0), (128, 0.5)), (257, 4104)),
+                                         (((8, 2.0), (16, -0.75), (40, 1.25)), (64, 136))])
+def test_fused_non_bf16_factors(ctx, fdt, ranks, shape):
+    """f16 factors on the f16 MFMA, FP8 factors widened to bf16 (exact) on the
+    bf16 MFMA: within the fused path's tolerance of the oracle, which widens
+    them as lora.rs:176-209 does; with LTXW_DESC_EXACT, bit-exact."""
+    log("case: factor type", fdt, ranks, shape)
+    rows, cols = shape
+    rng = np.random.default_rng(fdt * 1000 + rows)
+    case = synth.tensor_case(rows + cols + fdt, rows, cols, synth.E4M3FN, synth.SCALE_ROW, loras=())
+    case["loras"] = [(factor_codes(rng, fdt, (rows, r)), factor_codes(rng, fdt, (r, cols)), r, c, fdt) for r, c in ranks]
+    got, = run_grouped(ctx, [case])
+    U.compare_lora_bf16(case, got)
+    exact, = run_grouped(ctx, [case], flags=lw.DESC_EXACT)
+    assert np.array_equal(exact, U.oracle_bf16(case))
+
+
 def test_fused_f32_output(ctx):
     """f32 output (the reference's own HostTensor type): within the f32
     forward-error bound of both orders, 2*(rank+4)*2^-24*(|deq|+sum|cBA|)."""
