@@ -115,8 +115,9 @@ __global__ __launch_bounds__(256) void k_generic(GenericArgs g) {
 // owns columns i0 + 8*cg .. +7 of rows g0 + rs + 16*k, k < 4. Per LoRA, the
 // ranks go in chunks of 32: A[r][band] and B[rows][r] widened to f32 into
 // LDS, then every thread runs w = fma(coeff * B[o][r], A[r][i], w) in r order.
-// VALU-bound (r FMAs per element); for adapters whose factors are not bf16,
-// non-FP8 bases, odd shapes, and bit-exact requests.
+// VALU-bound (r FMAs per element); for f32 or mixed-type factors, non-FP8
+// bases, odd shapes, coefficients the MFMA path does not take, and bit-exact
+// requests.
 // ---------------------------------------------------------------------------
 constexpr int kExactR = 32;
 
