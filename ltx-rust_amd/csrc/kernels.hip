@@ -162,15 +162,20 @@ __global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
         acc[k][j] = (o < rows && i < cols) ? load_base(J, o * cols + i) : 0.0f;
       }
     }
-    if (o < rows) {
-      const float s = J.scale_mode == 0 ? 1.0f : J.scales[J.scale_mode == 2 ? o : 0];
+    // Uniform branches around whole loops (not selects per element).
+    if (o < rows && J.scale_mode != 0) {
+      const float s = J.scales[J.scale_mode == 2 ? o : 0];
+      if (g.plain_scale) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float v = acc[k][j];
-        if (J.scale_mode != 0) v = g.plain_scale ? s * v : __builtin_fmaf(s, v, 0.0f);
-        if (g.has_post) v = v * g.post_mul;
-        acc[k][j] = v;
+        for (int j = 0; j < 8; ++j) acc[k][j] = s * acc[k][j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[k][j] = __builtin_fmaf(s, acc[k][j], 0.0f);
       }
+    }
+    if (o < rows && g.has_post) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[k][j] = acc[k][j] * g.post_mul;
     }
   }
   for (int l = 0; l < J.n_loras && l < kMaxLoras; ++l) {
@@ -213,11 +218,37 @@ __global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
         // as the reference forms it before each row's FMA pass.
         const uint64_t oo = g0 + (tid >> 2);
         const int q0 = (tid & 3) * 8;
+        // 8 consecutive B elements: one (bf16) or two (f32) 16-byte loads when
+        // whole and aligned.
+        const bool b_vec = (FDT == 0 || FDT == 1) && oo < rows && r0 + q0 + 8 <= rank && (rank & 7) == 0 &&
+                           (((uintptr_t)L.b) & 15) == 0;
+        if (b_vec) {
+          float bv[8];
+          if constexpr (FDT == 0) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(L.b) + oo * rank + r0 + q0);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const uint64_t rq = r0 + q0 + q;
-          Bs[tid >> 2][q0 + q] =
-              (oo < rows && rq < rank) ? L.coeff * factor_at<FDT>(L.b, L.dtype, oo * rank + rq) : 0.0f;
+            for (int q = 0; q < 4; ++q) {
+              bv[2 * q] = __builtin_bit_cast(float, v[q] << 16);
+              bv[2 * q + 1] = __builtin_bit_cast(float, v[q] & 0xFFFF0000u);
+            }
+          } else if constexpr (FDT == 1) {
+            const f32x4* src = reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(L.b) + oo * rank + r0 + q0);
+            const f32x4 v0 = src[0], v1 = src[1];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              bv[q] = v0[q];
+              bv[4 + q] = v1[q];
+            }
+          }
+#pragma unroll
+          for (int q = 0; q < 8; ++q) Bs[tid >> 2][q0 + q] = L.coeff * bv[q];
+        } else {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const uint64_t rq = r0 + q0 + q;
+            Bs[tid >> 2][q0 + q] =
+                (oo < rows && rq < rank) ? L.coeff * factor_at<FDT>(L.b, L.dtype, oo * rank + rq) : 0.0f;
+          }
         }
       }
       __syncthreads();
@@ -254,9 +285,19 @@ __global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
         dst[0] = (f32x4){acc[k][0], acc[k][1], acc[k][2], acc[k][3]};
         dst[1] = (f32x4){acc[k][4], acc[k][5], acc[k][6], acc[k][7]};
       } else {
+        // The hardware pack is RNE; half's NaN rule (top payload bits, quiet
+        // bit set) is applied only when the wave holds a NaN.
         u32x4 v;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = (uint32_t)bf16_rne(acc[k][2 * q]) | ((uint32_t)bf16_rne(acc[k][2 * q + 1]) << 16);
+        for (int q = 0; q < 4; ++q) v[q] = pack_bf16(acc[k][2 * q], acc[k][2 * q + 1]);
+        uint64_t any = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) any |= __builtin_amdgcn_ballot_w64(__builtin_isnan(acc[k][j]));
+        if (any) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            v[q] = (uint32_t)bf16_rne(acc[k][2 * q]) | ((uint32_t)bf16_rne(acc[k][2 * q + 1]) << 16);
+        }
         *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(J.out) + o * cols + c0) = v;
       }
       continue;
