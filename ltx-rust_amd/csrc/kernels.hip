@@ -153,8 +153,7 @@ __global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
       const u32x2 wv = *reinterpret_cast<const u32x2*>(J.w + o * cols + c0);
       decode4(wv[0], J.fmt, acc[k]);
       decode4(wv[1], J.fmt, acc[k] + 4);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[k][j] = canon_nan(acc[k][j]);
+      canon_nan_wave<8>(acc[k]);
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -275,10 +274,7 @@ __global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
   for (int k = 0; k < 4; ++k) {
     const uint64_t o = g0 + rs + 16 * k;
     if (o >= rows) continue;
-    if (J.fmt <= 1) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[k][j] = canon_nan(acc[k][j]);
-    }
+    if (J.fmt <= 1) canon_nan_wave<8>(acc[k]);
     if (o_vec) {
       if (F32OUT) {
         f32x4* dst = reinterpret_cast<f32x4*>(reinterpret_cast<float*>(J.out) + o * cols + c0);
