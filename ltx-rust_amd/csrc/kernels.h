@@ -113,7 +113,8 @@ hipError_t launch_exact(const ExactArgs& a, bool f32out, hipStream_t stream);
 hipError_t launch_dequant(const DequantArgs& a, int fmt, int scale_mode, bool f32out,
                           hipStream_t stream);
 
-// Tiled dequant for tensors of up to kTileMaxElems elements: the fused
+// Tiled dequant for tensors of up to kTileMaxElems elements (an FFN matrix
+// of the DiT has 2^26): the fused
 // kernels' access pattern (pairs of 128-row x 128-column units per
 // workgroup, 8 FP8 bytes per lane and row) without the LoRA. Requirements
 // checked by the caller: cols % 8 == 0; w, out (and row scales) 16-byte
@@ -124,7 +125,7 @@ struct DequantTileArgs {
   const float* scales;
   uint32_t rows, cols, bands_n;
 };
-constexpr uint64_t kTileMaxElems = 1ull << 25;
+constexpr uint64_t kTileMaxElems = 1ull << 27;
 hipError_t launch_dequant_tile(const DequantTileArgs& a, int fmt, int scale_mode, bool f32out,
                                hipStream_t stream);
 

@@ -14,12 +14,15 @@ namespace ltxw {
 namespace {
 
 // ---------------------------------------------------------------------------
-// (a) Streaming dequant. Each thread handles kChunksPerThread chunks of 16
+// (a) Streaming dequant, for tensors above kTileMaxElems elements and the
+// unaligned or narrow ones. Each thread handles kChunksPerThread chunks of 16
 // FP8 bytes: one 128-bit load, two 128-bit bf16 stores (four for f32).
 // Loads are non-temporal (read once); stores are ordinary, which measured
-// faster than non-temporal stores for this kernel on MI355X.
+// faster than non-temporal stores for this kernel on MI355X. One chunk per
+// thread measured fastest on the large tensors this kernel takes
+// (65536 x 4096: 138 us against 145 with two and 149 with four).
 // ---------------------------------------------------------------------------
-constexpr int kChunksPerThread = 4;
+constexpr int kChunksPerThread = 1;
 
 template <int FMT, int SMODE, bool F32OUT>
 __global__ __launch_bounds__(256) void k_dequant(DequantArgs a) {
@@ -365,9 +368,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 3
 // column band; lane l of wave w handles, in each unit, the 8 columns
 // i0 + 8 (l % 16) .. +7 of rows r0 + 4 (l / 16) + {0..3, 16..19} with
 // r0 = g0 + 32 w. Both units' bytes are requested before the first unit is
-// converted. Faster than the streaming kernel on tensors of one layer's size
-// (a launch that is resident at once); the streaming kernel wins on larger
-// ones.
+// converted. Faster than the streaming kernel up to an FFN matrix
+// (4096 x 4096: 9.2 against 11.5 us; 16384 x 4096: 37.8 against 38.7 us with
+// the streaming kernel at its best setting).
 // ---------------------------------------------------------------------------
 template <int SMODE, bool FULL>
 __device__ __forceinline__ void dqt_load(const DequantTileArgs& a, uint32_t i0, uint32_t g0, int tid, u32x2 (&wv)[8],
