@@ -162,7 +162,9 @@ ltxw::JobDev to_job(const ltxw_tensor_desc& d) {
 
 // The tiled MFMA kernel's layout requirements (else: generic kernel).
 bool fused_ok(const ltxw_tensor_desc& d) {
-  if (ltxw::format_bytes(d.fmt) != 1) return false;
+  // FP8 bases; bf16 / f16 bases (no scale) when every factor is bf16.
+  const int fb = ltxw::format_bytes(d.fmt);
+  if (fb != 1 && !(fb == 2 && d.n_loras > 0 && d.loras[0].dtype == LTXW_FACTOR_BF16)) return false;
   if (d.cols % 8 != 0 || !aligned(d.w, 16) || !aligned(d.out, 16)) return false;
   if (d.scale_mode == LTXW_SCALE_ROW && !aligned(d.scales, 16)) return false;  // read 4 rows at a time
   // The kernel addresses every buffer with 32-bit byte offsets.
@@ -302,7 +304,7 @@ int job_k(const ltxw::JobDev& j) {
 // One fused launch over `jobs` (all fused_ok, same out dtype, kernel, factor
 // type and K-steps): one workgroup per 128-column band and 256 rows of every
 // job.
-int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool multi, int fdt) {
+int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool multi, int fdt, bool base16) {
   if (jobs.empty()) return LTXW_OK;
   int kmax = 0;
   for (auto& j : jobs) kmax = std::max(kmax, job_k(j));
@@ -336,7 +338,7 @@ int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool 
     t.jobs = reinterpret_cast<const ltxw::JobDev*>(slot->dev);
     t.begins = reinterpret_cast<const int64_t*>((char*)slot->dev + off_b);
   }
-  HIP_TRY(ctx, ltxw::launch_fused(t, f32out, multi, fdt, ctx->compute), "fused kernel launch");
+  HIP_TRY(ctx, ltxw::launch_fused(t, f32out, multi, fdt, base16, ctx->compute), "fused kernel launch");
   return LTXW_OK;
 }
 
@@ -349,12 +351,12 @@ int ltxw::run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n, const D
     int rc = check_desc(ctx, descs[k], &counts[(size_t)k]);
     if (rc) return rc;
   }
-  // Fused launches are bucketed by (f32 out, kernel, K-steps, factor type),
-  // so that the register arrays of each launch are sized for its own jobs'
-  // rank, not for the largest rank of the call. One bf16 LoRA takes the
-  // single-LoRA kernel; several LoRAs or other factor types the several-LoRA
-  // one.
-  std::map<std::tuple<int, int, int, int>, std::vector<ltxw::JobDev>> buckets;
+  // Fused launches are bucketed by (f32 out, kernel, K-steps, factor type,
+  // 16-bit base), so that the register arrays of each launch are sized for
+  // its own jobs' rank, not for the largest rank of the call. One bf16 LoRA
+  // on an FP8 base takes the single-LoRA kernel; several LoRAs, other factor
+  // types or bf16 / f16 bases the several-LoRA one.
+  std::map<std::tuple<int, int, int, int, int>, std::vector<ltxw::JobDev>> buckets;
   for (int k = 0; k < n; ++k) {
     const ltxw_tensor_desc& d = descs[k];
     uint64_t cnt = counts[(size_t)k];
@@ -368,13 +370,15 @@ int ltxw::run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n, const D
     } else {
       ltxw::JobDev j = to_job(d);
       const int fdt = d.loras[0].dtype;
-      const bool multi = d.n_loras > 1 || fdt != LTXW_FACTOR_BF16;
-      buckets[{d.out_dtype == LTXW_OUT_F32, multi, job_k(j) / 32, fdt}].push_back(j);
+      const bool base16 = ltxw::format_bytes(d.fmt) == 2;
+      const bool multi = d.n_loras > 1 || fdt != LTXW_FACTOR_BF16 || base16;
+      buckets[{d.out_dtype == LTXW_OUT_F32, multi, job_k(j) / 32, fdt, base16}].push_back(j);
     }
     if (rc) return rc;
   }
   for (auto& kv : buckets) {
-    int rc = run_fused(ctx, kv.second, std::get<0>(kv.first) == 1, std::get<1>(kv.first) == 1, std::get<3>(kv.first));
+    int rc = run_fused(ctx, kv.second, std::get<0>(kv.first) == 1, std::get<1>(kv.first) == 1, std::get<3>(kv.first),
+                       std::get<4>(kv.first) == 1);
     if (rc) return rc;
   }
   return LTXW_OK;

@@ -136,19 +136,22 @@ hipError_t launch_dequant_tile(const DequantTileArgs& a, int fmt, int scale_mode
 // adjacent 128-row units (kPairRows rows); unit_begin and total_units count
 // pairs. `multi`: the several-LoRA kernel (several LoRAs per tensor, or
 // factors other than bf16), whose jobs all have factors of element type
-// `fdt`. Every job's qmask, cmul, coeff_out and step[] are filled
-// (plan_fused in api.cpp).
-hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, int fdt, hipStream_t stream);
+// `fdt` and, with `base16`, bf16 / f16 bases. Every job's qmask, cmul,
+// coeff_out and step[] are filled (plan_fused in api.cpp).
+hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, int fdt, bool base16, hipStream_t stream);
 
 // The several-LoRA kernel alone (kernels_multi_dev.h); `ks` K-steps (1-7),
 // every job's factors of element type `fdt` (ltxw_factor_dtype: 0 bf16,
-// 2 f16, 3 e4m3fn, 4 e5m2). launch_fused calls it for `multi`.
-hipError_t launch_fused_multi(const JobTable& t, bool f32out, int ks, int fdt, hipStream_t stream);
+// 2 f16, 3 e4m3fn, 4 e5m2), bases FP8 or, with `base16`, bf16 / f16 (bf16
+// factors only). launch_fused calls it for `multi`.
+hipError_t launch_fused_multi(const JobTable& t, bool f32out, int ks, int fdt, bool base16, hipStream_t stream);
 // Its instantiations, one translation unit per factor type (kernels_multi_*.hip).
 hipError_t launch_fused_multi_bf16(const JobTable& t, bool f32out, int ks, hipStream_t stream);
 hipError_t launch_fused_multi_f16(const JobTable& t, bool f32out, int ks, hipStream_t stream);
 hipError_t launch_fused_multi_e4m3fn(const JobTable& t, bool f32out, int ks, hipStream_t stream);
 hipError_t launch_fused_multi_e5m2(const JobTable& t, bool f32out, int ks, hipStream_t stream);
+// bf16 / f16 bases (no scale) with bf16 factors (kernels_multi_b16.hip).
+hipError_t launch_fused_multi_base16(const JobTable& t, bool f32out, int ks, hipStream_t stream);
 
 // Rows of one workgroup of the single-LoRA kernel.
 constexpr int kPairRows = 2 * kWavesPerGroup * kStripRows;

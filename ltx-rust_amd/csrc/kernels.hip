@@ -528,11 +528,11 @@ hipError_t launch_fused_ks(const JobTable& t, bool f32out, dim3 grid, size_t lds
   return hipGetLastError();
 }
 
-hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, int fdt, hipStream_t stream) {
+hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, int fdt, bool base16, hipStream_t stream) {
   if (t.total_units == 0) return hipSuccess;
   dim3 grid((unsigned)t.total_units);
   const int ks = (t.lds_ld - 8) / 32;  // K-steps of the largest job
-  if (multi) return launch_fused_multi(t, f32out, ks, fdt, stream);
+  if (multi) return launch_fused_multi(t, f32out, ks, fdt, base16, stream);
   size_t lds = (size_t)kBandCols * (size_t)t.lds_ld * sizeof(uint16_t);
   switch (ks) {
     case 1: return launch_fused_ks<1>(t, f32out, grid, lds, stream);
@@ -546,7 +546,8 @@ hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, int fdt, hip
   }
 }
 
-hipError_t launch_fused_multi(const JobTable& t, bool f32out, int ks, int fdt, hipStream_t stream) {
+hipError_t launch_fused_multi(const JobTable& t, bool f32out, int ks, int fdt, bool base16, hipStream_t stream) {
+  if (base16) return fdt == 0 ? launch_fused_multi_base16(t, f32out, ks, stream) : hipErrorInvalidValue;
   switch (fdt) {
     case 0: return launch_fused_multi_bf16(t, f32out, ks, stream);
     case 2: return launch_fused_multi_f16(t, f32out, ks, stream);

@@ -255,8 +255,9 @@ __device__ __forceinline__ PJ pj_load(const JobTable& t, uint64_t unit) {
 
 template <int KS>
 struct Frag {
+  using Wv = u32x2;
   bf16x8 bf[KS][2];
-  u32x2 wv[8];
+  Wv wv[8];
   float sc[8];
 };
 template <int KS>
@@ -318,8 +319,12 @@ __device__ __forceinline__ void pp_issue_f(const PJ& J, uint32_t i0, uint32_t g0
 }
 
 // (FragT: any fragment set with the wv[8] / sc[8] members.)
+// The base bytes of 8 elements: u32x2 for FP8, u32x4 for 16-bit formats (the
+// type of FragT::wv's elements says which).
 template <int KS, bool FULL, class FragT>
 __device__ __forceinline__ void pp_issue_w(const PJ& J, uint32_t i0, uint32_t g0, int tid, FragT& f) {
+  using W = typename FragT::Wv;
+  constexpr uint32_t esz = sizeof(W) / 8;  // bytes per element
   const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
   const uint32_t rows = J.rows, cols = J.cols;
   const uint32_t r0 = g0 + kStripRows * wave;
@@ -330,8 +335,30 @@ __device__ __forceinline__ void pp_issue_w(const PJ& J, uint32_t i0, uint32_t g0
 #pragma unroll
   for (int g = 0; g < 8; ++g) {
     const uint32_t dr = 16 * (g >> 2) + (g & 3);
-    f.wv[g] = (u32x2){0u, 0u};
-    if (col_ok && (FULL || rl + dr < rows)) f.wv[g] = ld_nt_at<u32x2>(J.w, e0 + dr * cols);
+    f.wv[g] = W{};
+    if (col_ok && (FULL || rl + dr < rows)) f.wv[g] = ld_nt_at<W>(J.w, esz * (e0 + dr * cols));
+  }
+}
+
+// 8 base elements -> f32: FP8 through the hardware converts (FMT 0 e4m3fn,
+// 1 e5m2), bf16 (2) by a shift, f16 (3) by the hardware convert; all exact.
+template <int FMT, class W>
+__device__ __forceinline__ void decode8(const W& w, float* x) {
+  if constexpr (FMT <= 1) {
+    decode4(w[0], FMT, x);
+    decode4(w[1], FMT, x + 4);
+  } else if constexpr (FMT == 2) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      x[2 * q] = __builtin_bit_cast(float, w[q] << 16);
+      x[2 * q + 1] = __builtin_bit_cast(float, w[q] & 0xFFFF0000u);
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      x[2 * q] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[q] & 0xFFFFu));
+      x[2 * q + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[q] >> 16));
+    }
   }
 }
 
@@ -391,13 +418,14 @@ __device__ __forceinline__ void pp_epilogue(const PJ& J, const FragT& f, Acc<KS>
     for (int v = 0; v < 4; ++v) {
       const int g = 4 * mb + v;
       float x[8];
-      decode4(f.wv[g][0], FMT, x);
-      decode4(f.wv[g][1], FMT, x + 4);
+      decode8<FMT>(f.wv[g], x);
 #pragma unroll
       for (int j = 0; j < 8; ++j) a.v[mb][j][v] = __builtin_fmaf(f.sc[g], x[j], a.v[mb][j][v]);
     }
   }
-  {
+  // FP8 NaN codes decode to the reference's one NaN (f32::NAN); 16-bit bases
+  // keep what the arithmetic makes of theirs.
+  if constexpr (FMT <= 1) {
     uint64_t any = 0;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)

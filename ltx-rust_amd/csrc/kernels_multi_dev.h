@@ -3,6 +3,8 @@
 // translation unit, so that they compile in parallel. CDNA4 (gfx950, wave64).
 #pragma once
 
+#include <type_traits>
+
 #include "kernels_dev.h"
 
 namespace ltxw {
@@ -110,10 +112,12 @@ struct StageM {
   typename FactorRaw<FDT>::T lo[KS], hi[KS];
 };
 
-template <int KS, int FDT>
+// B16: the base is bf16 or f16 (16 bytes per 8 elements), else FP8.
+template <int KS, int FDT, bool B16>
 struct FragM {
+  using Wv = typename std::conditional<B16, u32x4, u32x2>::type;
   typename FactorRaw<FDT>::T bf[KS][2];
-  u32x2 wv[8];
+  Wv wv[8];
   float sc[8];
 };
 
@@ -150,8 +154,8 @@ __device__ __forceinline__ void pm_stage(const StageM<KS, FDT>& st, uint16_t* AT
   }
 }
 
-template <int KS, bool FULL, int FDT>
-__device__ __forceinline__ void pm_issue_f(const PJM<KS>& M, uint32_t g0, int tid, FragM<KS, FDT>& f) {
+template <int KS, bool FULL, int FDT, bool B16>
+__device__ __forceinline__ void pm_issue_f(const PJM<KS>& M, uint32_t g0, int tid, FragM<KS, FDT, B16>& f) {
   using R = typename FactorRaw<FDT>::T;
   constexpr uint32_t E = FactorRaw<FDT>::kBytes;
   const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
@@ -188,9 +192,9 @@ __device__ __forceinline__ void pm_issue_f(const PJM<KS>& M, uint32_t g0, int ti
   }
 }
 
-template <int KS, int FDT>
-__device__ __forceinline__ void pm_mfma(const PJM<KS>& M, const FragM<KS, FDT>& f, const uint16_t* AT, int ld, int tid,
-                                        Acc<KS>& a) {
+template <int KS, int FDT, bool B16>
+__device__ __forceinline__ void pm_mfma(const PJM<KS>& M, const FragM<KS, FDT, B16>& f, const uint16_t* AT, int ld,
+                                        int tid, Acc<KS>& a) {
   const int lane = tid & 63, ln = lane & 15, lg = lane >> 4;
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
@@ -219,9 +223,10 @@ template <bool F32OUT, int KS, int FMT, bool FULL, int FDT>
 __device__ __forceinline__ void pair_units_multi(const PJM<KS>& M, uint16_t* AT, uint32_t i0, uint32_t gA,
                                                  uint32_t gB, bool hasB, int tid) {
   constexpr int LD = 32 * KS + 8;
+  constexpr bool B16 = FMT >= 2;
   StageM<KS, FDT> st;
   pm_issue_a<KS, FDT>(M, i0, tid, st);
-  FragM<KS, FDT> fa, fb;
+  FragM<KS, FDT, B16> fa, fb;
   pm_issue_f<KS, FULL, FDT>(M, gA, tid, fa);
   pp_issue_w<KS, FULL>(M.base, i0, gA, tid, fa);
   pp_issue_w<KS, FULL>(M.base, i0, hasB ? gB : gA, tid, fb);
@@ -241,7 +246,7 @@ __device__ __forceinline__ void pair_units_multi(const PJM<KS>& M, uint16_t* AT,
   }
 }
 
-template <bool F32OUT, int KS, int FDT>
+template <bool F32OUT, int KS, int FDT, bool B16>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_fused_pair_multi(JobTable tab) {
   extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
   const int tid = threadIdx.x;
@@ -253,24 +258,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   const uint32_t gB = gA + kWavesPerGroup * kStripRows;
   const bool hasB = gB < M.base.rows;
   const bool full = gB + kWavesPerGroup * kStripRows <= M.base.rows && i0 + kBandCols <= M.base.cols;
-  if (M.base.fmt == 0) {
-    if (full) pair_units_multi<F32OUT, KS, 0, true, FDT>(M, AT, i0, gA, gB, hasB, tid);
-    else pair_units_multi<F32OUT, KS, 0, false, FDT>(M, AT, i0, gA, gB, hasB, tid);
+  // Base formats (ltxw_format): e4m3fn / e5m2, or with B16 bf16 / f16.
+  constexpr int F0 = B16 ? 2 : 0, F1 = B16 ? 3 : 1;
+  if (M.base.fmt == (uint32_t)F0) {
+    if (full) pair_units_multi<F32OUT, KS, F0, true, FDT>(M, AT, i0, gA, gB, hasB, tid);
+    else pair_units_multi<F32OUT, KS, F0, false, FDT>(M, AT, i0, gA, gB, hasB, tid);
   } else {
-    if (full) pair_units_multi<F32OUT, KS, 1, true, FDT>(M, AT, i0, gA, gB, hasB, tid);
-    else pair_units_multi<F32OUT, KS, 1, false, FDT>(M, AT, i0, gA, gB, hasB, tid);
+    if (full) pair_units_multi<F32OUT, KS, F1, true, FDT>(M, AT, i0, gA, gB, hasB, tid);
+    else pair_units_multi<F32OUT, KS, F1, false, FDT>(M, AT, i0, gA, gB, hasB, tid);
   }
 }
 
-template <int FDT>
+template <int FDT, bool B16 = false>
 hipError_t launch_multi_fdt(const JobTable& t, bool f32out, int ks, hipStream_t stream) {
   if (t.total_units == 0) return hipSuccess;
   dim3 grid((unsigned)t.total_units);
   size_t lds = (size_t)kBandCols * (size_t)t.lds_ld * sizeof(uint16_t);
 #define LTXW_MULTI_LAUNCH(KS)                                                                            \
   case KS:                                                                                               \
-    if (f32out) hipLaunchKernelGGL((k_fused_pair_multi<true, KS, FDT>), grid, dim3(256), lds, stream, t); \
-    else hipLaunchKernelGGL((k_fused_pair_multi<false, KS, FDT>), grid, dim3(256), lds, stream, t);       \
+    if (f32out) hipLaunchKernelGGL((k_fused_pair_multi<true, KS, FDT, B16>), grid, dim3(256), lds, stream, t); \
+    else hipLaunchKernelGGL((k_fused_pair_multi<false, KS, FDT, B16>), grid, dim3(256), lds, stream, t);       \
     break;
   switch (ks) {
     LTXW_MULTI_LAUNCH(1)

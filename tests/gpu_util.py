@@ -5,7 +5,7 @@ import numpy as np
 import ltx_weights as lw
 import oracle_lib as O
 
-FMT_TO_ORC = {lw.FMT_E4M3FN: O.E4M3FN, lw.FMT_E5M2: O.E5M2}
+FMT_TO_ORC = {lw.FMT_E4M3FN: O.E4M3FN, lw.FMT_E5M2: O.E5M2, lw.FMT_BF16: O.BF16, lw.FMT_F16: O.F16}
 # LoRA factor element types (a case's LoRA tuples are (B, A, rank, coeff) or
 # (B, A, rank, coeff, factor type); bf16 when absent).
 FDT_TO_ORC = {lw.FACTOR_BF16: O.BF16, lw.FACTOR_F32: O.F32, lw.FACTOR_F16: O.F16,

@@ -151,7 +151,9 @@ def base_bits(rng, dt, shape):
 ])
 def test_reference_order_paths_bit_exact(ctx, tmp, base_dt, factor_dt, ranks, shape, scale):
     """Every path that keeps the reference's operation order matches the
-    oracle's f32 bit for bit (and its bf16 rounding)."""
+    oracle's f32 bit for bit (and its bf16 rounding): the tensors the MFMA
+    kernels do not take, and, with MAT_EXACT, those they do (here the bf16
+    base with bf16 factors)."""
     log("reference-order case", base_dt, factor_dt, ranks, shape, scale)
     rng = np.random.default_rng(hash((base_dt, factor_dt, tuple(ranks), shape)) % (1 << 31))
     rows, cols = shape
@@ -175,10 +177,10 @@ def test_reference_order_paths_bit_exact(ctx, tmp, base_dt, factor_dt, ranks, sh
         loras.append((b.reshape(rows, r), a.reshape(r, cols), FACTOR_DT[factor_dt], O.lora_coeff(strength, None, r)))
     smode = {None: O.SCALE_NONE, "row": O.SCALE_ROW, "tensor": O.SCALE_TENSOR}[scale]
     want = O.read_f32(w.reshape(rows, cols), O.DTYPE_CODES[base_dt], smode, sc, loras)
-    got = store.read("t.weight", ctx)[1]
+    got = store.read("t.weight", ctx, flags=MAT_EXACT)[1]
     assert np.array_equal(bits(got), bits(want))
     # bf16 materialisation of the same key = RNE of that f32.
-    out = store.materialize_bf16(ctx, ["t.weight"])["t.weight"]
+    out = store.materialize_bf16(ctx, ["t.weight"], flags=MAT_EXACT)["t.weight"]
     try:
         assert np.array_equal(out.to_numpy(), O.read_bf16(w.reshape(rows, cols), O.DTYPE_CODES[base_dt], smode, sc,
                                                           loras))
@@ -522,3 +524,39 @@ def test_materialise_small_staging_slots_many_tensors(tmp):
         finally:
             for t in outs.values():
                 t.free()
+
+
+@pytest.mark.parametrize("base_dt", ["BF16", "F16"])
+@pytest.mark.parametrize("ranks,shape", [([64], (256, 512)), ([32, 16], (130, 264))])
+def test_16bit_base_fused_path(ctx, tmp, base_dt, ranks, shape):
+    """bf16 / f16 bases with bf16 LoRAs run on the several-LoRA MFMA kernel:
+    within the fused tolerance of the oracle by default, bit-exact with
+    MAT_EXACT."""
+    log("16-bit base fused", base_dt, ranks, shape)
+    rng = np.random.default_rng(77 + len(ranks))
+    rows, cols = shape
+    w = base_bits(rng, base_dt, (rows, cols))
+    store = WeightStore.open([tmp([("t.weight", base_dt, [rows, cols], w)])])
+    loras = []
+    for k, r in enumerate(ranks):
+        a = factor_bits(rng, "BF16", (r, cols), 0.05)
+        b = factor_bits(rng, "BF16", (rows, r), 0.05)
+        strength = [1.0, 0.5][k]
+        store.merge_lora(LoraFile.open(tmp([("t.lora_A.weight", "BF16", [r, cols], a),
+                                            ("t.lora_B.weight", "BF16", [rows, r], b)])), strength)
+        loras.append((b.reshape(rows, r), a.reshape(r, cols), O.lora_coeff(strength, None, r)))
+    case = {"w": w.reshape(rows, cols), "scales": None, "rows": rows, "cols": cols, "scale_mode": O.SCALE_NONE,
+            "fmt": {"BF16": lw.FMT_BF16, "F16": lw.FMT_F16}[base_dt],
+            "loras": [(b, a, b.shape[1], c) for (b, a, c) in loras]}
+    out = store.materialize_bf16(ctx, ["t.weight"])["t.weight"]
+    try:
+        U.compare_lora_bf16(case, out.to_numpy())
+    finally:
+        out.free()
+    want = O.read_bf16(case["w"], O.DTYPE_CODES[base_dt], O.SCALE_NONE, None,
+                       [(b, a, O.BF16, c) for (b, a, c) in loras])
+    out = store.materialize_bf16(ctx, ["t.weight"], flags=MAT_EXACT)["t.weight"]
+    try:
+        assert np.array_equal(out.to_numpy(), want)
+    finally:
+        out.free()
