@@ -345,6 +345,8 @@ int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool 
 }  // namespace
 
 int ltxw::run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n, const DescEx* ex) {
+  // Job tables are allocated on the calling thread's current device.
+  HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
   // Validate everything before queuing anything.
   std::vector<uint64_t> counts((size_t)n);
   for (int k = 0; k < n; ++k) {
@@ -511,6 +513,7 @@ int ltxw_free(ltxw_ctx* ctx, void* dptr) {
 int ltxw_memset(ltxw_ctx* ctx, void* dptr, int value, size_t bytes) {
   if (!ctx || (!dptr && bytes)) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context or pointer");
   if (bytes == 0) return LTXW_OK;
+  if (int rc = check_extent(ctx, dptr, bytes, "memset destination")) return rc;
   HIP_TRY(ctx, hipMemsetAsync(dptr, value, bytes, ctx->compute), "hipMemsetAsync");
   return LTXW_OK;
 }
@@ -519,6 +522,8 @@ int ltxw_upload(ltxw_ctx* ctx, const void* host_src, size_t bytes, void* dst) {
   if (!ctx) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context");
   if (bytes == 0) return LTXW_OK;
   if (!host_src || !dst) return fail(ctx, LTXW_ERR_INVALID_ARG, "null source or destination");
+  if (int rc = check_extent(ctx, dst, bytes, "upload destination")) return rc;
+  HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
   if (int rc = ltxw::ensure_staging(ctx)) return rc;
   const char* src = (const char*)host_src;
   size_t done = 0;
@@ -544,6 +549,8 @@ int ltxw_download(ltxw_ctx* ctx, const void* src, size_t bytes, void* host_dst) 
   if (!ctx) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context");
   if (bytes == 0) return LTXW_OK;
   if (!src || !host_dst) return fail(ctx, LTXW_ERR_INVALID_ARG, "null source or destination");
+  if (int rc = check_extent(ctx, src, bytes, "download source")) return rc;
+  HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
   HIP_TRY(ctx, hipStreamSynchronize(ctx->compute), "synchronize before download");
   HIP_TRY(ctx, hipMemcpy(host_dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
   return LTXW_OK;

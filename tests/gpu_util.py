@@ -140,8 +140,8 @@ def compare_lora_bf16(case, got, row_sel=None):
     fin = np.isfinite(w64) & np.isfinite(g64)
     r64 = bf16_to_f64(bf16_from_f64_exact(w64))
     den = np.linalg.norm(w64[fin])
-    stats["frob_vs_rne_f64"] = float(np.linalg.norm((g64 - r64)[fin]) / den) if den else 0.0
-    stats["frob_vs_f64"] = float(np.linalg.norm((g64 - w64)[fin]) / den) if den else 0.0
+    stats["frob_vs_rne_f64"] = float(np.linalg.norm(g64[fin] - r64[fin]) / den) if den else 0.0
+    stats["frob_vs_f64"] = float(np.linalg.norm(g64[fin] - w64[fin]) / den) if den else 0.0
     assert stats["frob_vs_rne_f64"] <= 1e-3, stats
     return stats
 

@@ -325,6 +325,12 @@ def test_undersized_buffers_rejected_before_launch(ctx):
             ctx.dequant_lora(big, 64, 64, E4, NONE, None, [(big, small, 64, 1.0)], big)
         with pytest.raises(lw.InvalidArgument, match="weight"):
             ctx.dequant(big + (1 << 20) - 100, 1, 200, E4, NONE, None, big)
+        with pytest.raises(lw.InvalidArgument, match="upload destination"):
+            ctx.upload(np.zeros(1 << 16, np.uint8), small)
+        with pytest.raises(lw.InvalidArgument, match="download source"):
+            ctx.download(small, np.empty(1 << 16, np.uint8))
+        with pytest.raises(lw.InvalidArgument, match="memset destination"):
+            ctx.memset(small, 0, 1 << 16)
         ctx.synchronize()
     finally:
         ctx.free(small)
