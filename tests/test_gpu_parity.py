@@ -337,6 +337,36 @@ def test_undersized_buffers_rejected_before_launch(ctx):
         ctx.free(big)
 
 
+def test_tensor_beyond_32bit_byte_offsets(ctx):
+    """A 16392 x 65536 e5m2 tensor (2^30 + 2^19 elements, every byte value,
+    NaN codes included) with per-row scales and f32 output: 4 GiB of output,
+    byte offsets past 2^32. Without a LoRA it takes the linear dequant kernel
+    (above the tiled kernel's 2^27 elements); with a rank-16 LoRA the
+    reference-order kernel (past the fused kernels' 32-bit offsets). The first,
+    second and last rows and 30 sampled ones match the oracle bit for bit."""
+    log("case: 16392 x 65536 e5m2, f32 out")
+    rows, cols = 16392, 65536
+    rng = np.random.default_rng(9090)
+    w = rng.integers(0, 256, size=(rows, cols), dtype=np.uint8)
+    b, a = synth.lora_factors(rng, rows, cols, 16)
+    case = {"w": w, "scales": synth.scales(rng, rows, synth.SCALE_ROW), "loras": [], "rows": rows, "cols": cols,
+            "fmt": synth.E5M2, "scale_mode": synth.SCALE_ROW}
+    sel = np.unique(np.concatenate([[0, 1, rows - 1], rng.choice(rows, 30, replace=False)]))
+    d = U.Dev(ctx, case, lw.OUT_F32)
+    try:
+        for loras in ([], [(b, a, 16, 0.75)]):
+            case["loras"] = loras
+            d.loras = [(d._put(lb), d._put(la), r, c, lw.FACTOR_BF16) for (lb, la, r, c) in loras]
+            d.run()
+            got = np.empty((len(sel), cols), np.float32)
+            for k, r in enumerate(sel):
+                ctx.download(d.out + int(r) * cols * 4, got[k])
+            ref = U.oracle_f32(case, row_sel=sel)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), "n_loras %d" % len(loras)
+    finally:
+        d.free()
+
+
 def test_upload_download_round_trip(ctx):
     log("case: round trip")
     rng = np.random.default_rng(1)
