@@ -405,9 +405,11 @@ def main():
                 d["flags"] = lw.DESC_EXACT
     log(f"{n_inst} rotating instances")
     ctx.synchronize()
+    # Descriptor arrays marshalled once: a step is one call into the library.
+    descs = [ctx.make_descs(inst) for inst in insts]
 
     def step(k):
-        ctx.grouped(insts[k % n_inst])
+        ctx.grouped(descs[k % n_inst])
 
     # Plain device copy ceiling on the same stream (read + write bytes / time).
     cp_n = 512 << 20

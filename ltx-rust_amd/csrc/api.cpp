@@ -200,6 +200,9 @@ void plan_fused(ltxw::JobDev& j) {
     const ltxw::LoraDev& L = j.lora[l];
     const int nks = ltxw::pad_rank(L.rank) / 32;
     const size_t esz = (size_t)factor_bytes(L.dtype);
+    // B rows whose 64-byte K-step pieces all fall at one offset of their
+    // 128-byte lines: pair the steps for the B-fragment swap.
+    const bool swap = esz == 2 && (L.rank * esz) % 128 == 0;
     for (int kt = 0; kt < nks && t < ltxw::kMaxSteps; ++kt, ++t) {
       ltxw::StepDev& s = j.step[t];
       s.a = (const char*)L.a + esz * 32 * kt * (size_t)j.cols;
@@ -207,7 +210,7 @@ void plan_fused(ltxw::JobDev& j) {
       s.rank = (uint32_t)L.rank;
       s.klim = (uint32_t)(L.rank - 32 * kt);
       s.q = 1.0f;
-      s.pad = 0;
+      s.pair = swap && kt % 2 == 0 && kt + 1 < nks ? 1u : 0u;
     }
     if (l + 1 < j.n_loras && t >= 1) {
       j.step[t - 1].q = L.coeff / j.lora[l + 1].coeff;

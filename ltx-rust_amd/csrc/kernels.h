@@ -36,7 +36,9 @@ struct StepDev {
   uint32_t rank;      // the LoRA's rank
   uint32_t klim;      // ranks of the step that exist: rank - 32 kt (>= 32: all)
   float q;            // factor applied to the accumulator after the step
-  uint32_t pad;
+  uint32_t pair;      // 1: this step and the next, both whole and of one LoRA with
+                      // 16-bit factors and a row stride of a multiple of 128 bytes,
+                      // may swap their B pieces on odd rows (kSwapMinGrid launches)
 };
 constexpr int kMaxSteps = kRankMax / 32;
 

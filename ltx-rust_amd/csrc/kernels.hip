@@ -312,22 +312,22 @@ __global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
 }
 
 // Two vertically adjacent units of one band (rows [gA, gA + 256)).
-template <bool F32OUT, int KS, int FMT, bool FULL>
+template <bool F32OUT, int KS, int FMT, bool FULL, bool BSW>
 __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i0, uint32_t gA, uint32_t gB,
                                            bool hasB, int tid) {
   constexpr int LD = 32 * KS + 8;
   Stage<KS> st;
   pp_issue_a<KS>(J, i0, tid, st);
   Frag<KS> fa, fb;
-  pp_issue_f<KS, FULL>(J, i0, gA, tid, fa);
+  pp_issue_f<KS, FULL, BSW>(J, i0, gA, tid, fa);
   pp_issue_w<KS, FULL>(J, i0, gA, tid, fa);
   pp_issue_w<KS, FULL>(J, i0, hasB ? gB : gA, tid, fb);
   pp_stage<KS>(st, AT, LD, tid);
   __syncthreads();
   {
     Acc<KS> acc;
-    pp_mfma<KS>(fa, AT, LD, tid, acc);
-    pp_issue_f<KS, FULL>(J, i0, hasB ? gB : gA, tid, fb);
+    pp_mfma<KS, BSW>(J, fa, AT, LD, tid, acc);
+    pp_issue_f<KS, FULL, BSW>(J, i0, hasB ? gB : gA, tid, fb);
     pp_epilogue<F32OUT, KS, FULL, FMT>(J, fa, acc, i0, gA, tid);
   }
   // Re-read the A^T fragments for the second unit rather than keeping them
@@ -335,13 +335,14 @@ __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i
   asm volatile("" ::: "memory");
   if (hasB) {
     Acc<KS> acc;
-    pp_mfma<KS>(fb, AT, LD, tid, acc);
+    pp_mfma<KS, BSW>(J, fb, AT, LD, tid, acc);
     pp_epilogue<F32OUT, KS, FULL, FMT>(J, fb, acc, i0, gB, tid);
   }
 }
 
-// One workgroup per unit pair; the jobs' unit_begin count pairs.
-template <bool F32OUT, int KS>
+// One workgroup per unit pair; the jobs' unit_begin count pairs. BSW: the
+// B-fragment pair swap (launches of kSwapMinGrid workgroups and more).
+template <bool F32OUT, int KS, bool BSW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 3 : 2))) void k_fused_pair(JobTable tab) {
   extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
   const int tid = threadIdx.x;
@@ -354,11 +355,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 3
   const bool hasB = gB < J.rows;
   const bool full = gB + kWavesPerGroup * kStripRows <= J.rows && i0 + kBandCols <= J.cols;
   if (J.fmt == 0) {
-    if (full) pair_units<F32OUT, KS, 0, true>(J, AT, i0, gA, gB, hasB, tid);
-    else pair_units<F32OUT, KS, 0, false>(J, AT, i0, gA, gB, hasB, tid);
+    if (full) pair_units<F32OUT, KS, 0, true, BSW>(J, AT, i0, gA, gB, hasB, tid);
+    else pair_units<F32OUT, KS, 0, false, BSW>(J, AT, i0, gA, gB, hasB, tid);
   } else {
-    if (full) pair_units<F32OUT, KS, 1, true>(J, AT, i0, gA, gB, hasB, tid);
-    else pair_units<F32OUT, KS, 1, false>(J, AT, i0, gA, gB, hasB, tid);
+    if (full) pair_units<F32OUT, KS, 1, true, BSW>(J, AT, i0, gA, gB, hasB, tid);
+    else pair_units<F32OUT, KS, 1, false, BSW>(J, AT, i0, gA, gB, hasB, tid);
   }
 }
 
@@ -523,8 +524,16 @@ hipError_t launch_dequant_tile(const DequantTileArgs& a, int fmt, int scale_mode
 
 template <int KS>
 hipError_t launch_fused_ks(const JobTable& t, bool f32out, dim3 grid, size_t lds, hipStream_t stream) {
-  if (f32out) hipLaunchKernelGGL((k_fused_pair<true, KS>), grid, dim3(256), lds, stream, t);
-  else hipLaunchKernelGGL((k_fused_pair<false, KS>), grid, dim3(256), lds, stream, t);
+  // The swap pairs the K-steps of one LoRA: an even number of them.
+  if constexpr (KS % 2 == 0) {
+    if (t.total_units >= kSwapMinGrid) {
+      if (f32out) hipLaunchKernelGGL((k_fused_pair<true, KS, true>), grid, dim3(256), lds, stream, t);
+      else hipLaunchKernelGGL((k_fused_pair<false, KS, true>), grid, dim3(256), lds, stream, t);
+      return hipGetLastError();
+    }
+  }
+  if (f32out) hipLaunchKernelGGL((k_fused_pair<true, KS, false>), grid, dim3(256), lds, stream, t);
+  else hipLaunchKernelGGL((k_fused_pair<false, KS, false>), grid, dim3(256), lds, stream, t);
   return hipGetLastError();
 }
 

@@ -129,6 +129,11 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* G(T* p) {
 // keep the dispatch order: measured 2-5% faster there (one 4096 x 4096 layer
 // 12.5 -> 11.9 us), while the remap wins from about a DiT block up.
 constexpr uint32_t kRemapMinGrid = 2048;
+// Launches of at least this many workgroups use the B-fragment pair swap
+// (BSW, below): measured 1-3% faster per DiT block at rank 64 and 5-7% at
+// rank 128, against 0.3-1 us slower on one 4096 x 4096 layer (512
+// workgroups) and no gain at 2048.
+constexpr int64_t kSwapMinGrid = 3072;
 __device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t n) {
   if (n <= kRemapMinGrid) return bid;
   constexpr uint32_t kXcd = 8;
@@ -283,14 +288,31 @@ __device__ __forceinline__ void pp_issue_a(const PJ& J, uint32_t i0, int tid, St
   }
 }
 
-template <int KS, bool FULL>
+// B-fragment pair swap (BSW). One B-fragment load covers 16 rows x 64 bytes
+// (a K-step of 32 bf16 ranks). When the row stride (rank x 2 bytes) is a
+// multiple of 128, those 16 pieces sit at the same offset in their 128-byte
+// lines, and such loads measured 7% slower per DiT block at rank 128 than
+// with a padded stride. With the swap, the two loads of a step pair (t, t ^ 1)
+// fetch step t ^ 1's piece on odd rows instead, so each load alternates
+// between the two halves of the lines; the MFMA takes each odd row's operand
+// from its partner's register. Same data, same arithmetic: the output is
+// bit-identical. It costs a little in a launch that runs as one round of
+// workgroups, so it is used from kSwapMinGrid workgroups up.
+template <int KS, bool BSW>
+__device__ __forceinline__ bool pp_swap_lane(const PJ& J, int ln) {
+  if constexpr (BSW && KS % 2 == 0) return (J.rank % 64 == 0) && (ln & 1);
+  else return false;
+}
+
+template <int KS, bool FULL, bool BSW = false>
 __device__ __forceinline__ void pp_issue_f(const PJ& J, uint32_t i0, uint32_t g0, int tid, Frag<KS>& f) {
   const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
   const uint32_t rows = J.rows;
   const uint32_t r0 = g0 + kStripRows * wave;
+  const bool swl = pp_swap_lane<KS, BSW>(J, ln);
 #pragma unroll
   for (int t = 0; t < KS; ++t) {
-    const uint32_t kk = 32 * t + 8 * lg;
+    const uint32_t kk = 32 * (swl ? (t ^ 1) : t) + 8 * lg;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       const uint32_t ob = r0 + 16 * mb + ln;
@@ -380,21 +402,46 @@ struct Acc {
   f32x4 v[2][8];
 };
 
-template <int KS>
-__device__ __forceinline__ void pp_mfma(const Frag<KS>& f, const uint16_t* AT, int ld, int tid, Acc<KS>& a) {
+// K-step T of the swapped MFMA chain (template recursion keeps every register
+// index a compile-time constant; a computed index would put Frag in scratch).
+template <int T, int KS>
+__device__ __forceinline__ void pp_mfma_swapped(const Frag<KS>& f, const uint16_t* AT, int ld, int ln, int lg,
+                                                bool swl, Acc<KS>& a) {
+  if constexpr (T < KS) {
+    constexpr int TP = T ^ 1;  // KS is even
+    const bf16x8 b0 = swl ? f.bf[TP][0] : f.bf[T][0];
+    const bf16x8 b1 = swl ? f.bf[TP][1] : f.bf[T][1];
+    const int kk = 32 * T + 8 * lg;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+      const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + kk]);
+      a.v[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b0, at, a.v[0][nb], 0, 0, 0);
+      a.v[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b1, at, a.v[1][nb], 0, 0, 0);
+    }
+    pp_mfma_swapped<T + 1, KS>(f, AT, ld, ln, lg, swl, a);
+  }
+}
+
+template <int KS, bool BSW = false>
+__device__ __forceinline__ void pp_mfma(const PJ& J, const Frag<KS>& f, const uint16_t* AT, int ld, int tid,
+                                        Acc<KS>& a) {
   const int lane = tid & 63, ln = lane & 15, lg = lane >> 4;
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) a.v[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  if constexpr (BSW && KS % 2 == 0) {
+    pp_mfma_swapped<0, KS>(f, AT, ld, ln, lg, pp_swap_lane<KS, BSW>(J, ln), a);
+  } else {
 #pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    const int kk = 32 * t + 8 * lg;
+    for (int t = 0; t < KS; ++t) {
+      const int kk = 32 * t + 8 * lg;
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + kk]);
-      a.v[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][0], at, a.v[0][nb], 0, 0, 0);
-      a.v[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][1], at, a.v[1][nb], 0, 0, 0);
+      for (int nb = 0; nb < 8; ++nb) {
+        const bf16x8 at = *reinterpret_cast<const bf16x8*>(&AT[(nb * 16 + ln) * ld + kk]);
+        a.v[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][0], at, a.v[0][nb], 0, 0, 0);
+        a.v[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.bf[t][1], at, a.v[1][nb], 0, 0, 0);
+      }
     }
   }
 }

@@ -73,9 +73,10 @@ struct PJM {
   uint32_t klim[KS];
   float q[KS];
   uint32_t qmask;
+  uint32_t pf;  // bit t: steps t and t + 1 swap their B pieces on odd rows (BSW launches)
 };
 
-template <int KS>
+template <int KS, bool BSW>
 __device__ __forceinline__ PJM<KS> pjm_load(const JobTable& t, uint64_t unit) {
   JobDev J;
   load_job(t, unit, J);
@@ -104,6 +105,11 @@ __device__ __forceinline__ PJM<KS> pjm_load(const JobTable& t, uint64_t unit) {
     m.q[s] = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.step[s].q)));
   }
   m.qmask = uni(J.qmask);
+  m.pf = 0;
+  if constexpr (BSW) {
+#pragma unroll
+    for (int s = 0; s + 1 < KS; ++s) m.pf |= (uni(J.step[s].pair) & 1u) << s;
+  }
   return m;
 }
 
@@ -154,7 +160,7 @@ __device__ __forceinline__ void pm_stage(const StageM<KS, FDT>& st, uint16_t* AT
   }
 }
 
-template <int KS, bool FULL, int FDT, bool B16>
+template <int KS, bool FULL, int FDT, bool B16, bool BSW>
 __device__ __forceinline__ void pm_issue_f(const PJM<KS>& M, uint32_t g0, int tid, FragM<KS, FDT, B16>& f) {
   using R = typename FactorRaw<FDT>::T;
   constexpr uint32_t E = FactorRaw<FDT>::kBytes;
@@ -162,13 +168,35 @@ __device__ __forceinline__ void pm_issue_f(const PJM<KS>& M, uint32_t g0, int ti
   const uint32_t rows = M.base.rows;
   const uint32_t r0 = g0 + kStripRows * wave;
   const uint32_t kk = 8 * lg;
+  if constexpr (BSW) {
+    // The B-fragment pair swap of pp_issue_f (kernels_dev.h), with the pairs
+    // from the host: for a pair (t, t + 1) of one LoRA (pf bit t), odd rows
+    // fetch the other step's piece of their own row (both steps are whole,
+    // so the piece exists); pm_mfma_at swaps the operands back.
+    const bool odd = ln & 1;
 #pragma unroll
-  for (int t = 0; t < KS; ++t) {
+    for (int t = 0; t < KS; ++t) {
+      const bool first = t + 1 < KS && ((M.pf >> t) & 1u);
+      const bool second = t >= 1 && ((M.pf >> (t - 1)) & 1u);
+      const int64_t d = odd ? (first ? 32 * (int64_t)E : (second ? -32 * (int64_t)E : 0)) : 0;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      const uint32_t ob = r0 + 16 * mb + ln;
-      f.bf[t][mb] = R{};
-      if (kk < M.klim[t] && (FULL || ob < rows)) f.bf[t][mb] = ld_at<R>(M.b[t], E * (ob * M.rank[t] + kk));
+      for (int mb = 0; mb < 2; ++mb) {
+        const uint32_t ob = r0 + 16 * mb + ln;
+        f.bf[t][mb] = R{};
+        if (kk < M.klim[t] && (FULL || ob < rows))
+          f.bf[t][mb] = *reinterpret_cast<const __attribute__((address_space(1))) R*>(
+              (const __attribute__((address_space(1))) char*)M.b[t] + (int64_t)(E * (ob * M.rank[t] + kk)) + d);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const uint32_t ob = r0 + 16 * mb + ln;
+        f.bf[t][mb] = R{};
+        if (kk < M.klim[t] && (FULL || ob < rows)) f.bf[t][mb] = ld_at<R>(M.b[t], E * (ob * M.rank[t] + kk));
+      }
     }
   }
   const uint32_t rl = r0 + 4 * lg;
@@ -192,7 +220,46 @@ __device__ __forceinline__ void pm_issue_f(const PJM<KS>& M, uint32_t g0, int ti
   }
 }
 
-template <int KS, int FDT, bool B16>
+// K-step T of the swapped chain (template recursion: every register index is
+// a compile-time constant, so FragM stays in registers).
+template <int T, int KS, int FDT, bool B16>
+__device__ __forceinline__ void pm_mfma_at(const PJM<KS>& M, const FragM<KS, FDT, B16>& f, const uint16_t* AT,
+                                           int ld, int ln, int lg, Acc<KS>& a) {
+  if constexpr (T < KS) {
+    using R = typename FactorRaw<FDT>::T;
+    const bool odd = ln & 1;
+    R r0 = f.bf[T][0], r1 = f.bf[T][1];
+    if constexpr (T + 1 < KS) {
+      if ((M.pf >> T) & 1u) {
+        r0 = odd ? f.bf[T + 1][0] : r0;
+        r1 = odd ? f.bf[T + 1][1] : r1;
+      }
+    }
+    if constexpr (T >= 1) {
+      if ((M.pf >> (T - 1)) & 1u) {
+        r0 = odd ? f.bf[T - 1][0] : r0;
+        r1 = odd ? f.bf[T - 1][1] : r1;
+      }
+    }
+    const int kk = 32 * T + 8 * lg;
+    const u32x4 b0 = to_pairs<FDT>(r0), b1 = to_pairs<FDT>(r1);
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+      const u32x4 at = *reinterpret_cast<const u32x4*>(&AT[(nb * 16 + ln) * ld + kk]);
+      a.v[0][nb] = mfma_step<FDT>(b0, at, a.v[0][nb]);
+      a.v[1][nb] = mfma_step<FDT>(b1, at, a.v[1][nb]);
+    }
+    if (T + 1 < KS && (M.qmask & (1u << T))) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) a.v[mb][nb] *= M.q[T];
+    }
+    pm_mfma_at<T + 1, KS, FDT, B16>(M, f, AT, ld, ln, lg, a);
+  }
+}
+
+template <int KS, int FDT, bool B16, bool BSW>
 __device__ __forceinline__ void pm_mfma(const PJM<KS>& M, const FragM<KS, FDT, B16>& f, const uint16_t* AT, int ld,
                                         int tid, Acc<KS>& a) {
   const int lane = tid & 63, ln = lane & 15, lg = lane >> 4;
@@ -200,26 +267,30 @@ __device__ __forceinline__ void pm_mfma(const PJM<KS>& M, const FragM<KS, FDT, B
   for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) a.v[mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  if constexpr (BSW) {
+    pm_mfma_at<0, KS, FDT, B16>(M, f, AT, ld, ln, lg, a);
+  } else {
 #pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    const int kk = 32 * t + 8 * lg;
-    const u32x4 b0 = to_pairs<FDT>(f.bf[t][0]), b1 = to_pairs<FDT>(f.bf[t][1]);
+    for (int t = 0; t < KS; ++t) {
+      const int kk = 32 * t + 8 * lg;
+      const u32x4 b0 = to_pairs<FDT>(f.bf[t][0]), b1 = to_pairs<FDT>(f.bf[t][1]);
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      const u32x4 at = *reinterpret_cast<const u32x4*>(&AT[(nb * 16 + ln) * ld + kk]);
-      a.v[0][nb] = mfma_step<FDT>(b0, at, a.v[0][nb]);
-      a.v[1][nb] = mfma_step<FDT>(b1, at, a.v[1][nb]);
-    }
-    if (t + 1 < KS && (M.qmask & (1u << t))) {
+      for (int nb = 0; nb < 8; ++nb) {
+        const u32x4 at = *reinterpret_cast<const u32x4*>(&AT[(nb * 16 + ln) * ld + kk]);
+        a.v[0][nb] = mfma_step<FDT>(b0, at, a.v[0][nb]);
+        a.v[1][nb] = mfma_step<FDT>(b1, at, a.v[1][nb]);
+      }
+      if (t + 1 < KS && (M.qmask & (1u << t))) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+        for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) a.v[mb][nb] *= M.q[t];
+          for (int nb = 0; nb < 8; ++nb) a.v[mb][nb] *= M.q[t];
+      }
     }
   }
 }
 
-template <bool F32OUT, int KS, int FMT, bool FULL, int FDT>
+template <bool F32OUT, int KS, int FMT, bool FULL, int FDT, bool BSW>
 __device__ __forceinline__ void pair_units_multi(const PJM<KS>& M, uint16_t* AT, uint32_t i0, uint32_t gA,
                                                  uint32_t gB, bool hasB, int tid) {
   constexpr int LD = 32 * KS + 8;
@@ -227,31 +298,33 @@ __device__ __forceinline__ void pair_units_multi(const PJM<KS>& M, uint16_t* AT,
   StageM<KS, FDT> st;
   pm_issue_a<KS, FDT>(M, i0, tid, st);
   FragM<KS, FDT, B16> fa, fb;
-  pm_issue_f<KS, FULL, FDT>(M, gA, tid, fa);
+  pm_issue_f<KS, FULL, FDT, B16, BSW>(M, gA, tid, fa);
   pp_issue_w<KS, FULL>(M.base, i0, gA, tid, fa);
   pp_issue_w<KS, FULL>(M.base, i0, hasB ? gB : gA, tid, fb);
   pm_stage<KS, FDT>(st, AT, LD, tid);
   __syncthreads();
   {
     Acc<KS> acc;
-    pm_mfma<KS, FDT>(M, fa, AT, LD, tid, acc);
-    pm_issue_f<KS, FULL, FDT>(M, hasB ? gB : gA, tid, fb);
+    pm_mfma<KS, FDT, B16, BSW>(M, fa, AT, LD, tid, acc);
+    pm_issue_f<KS, FULL, FDT, B16, BSW>(M, hasB ? gB : gA, tid, fb);
     pp_epilogue<F32OUT, KS, FULL, FMT>(M.base, fa, acc, i0, gA, tid);
   }
   asm volatile("" ::: "memory");
   if (hasB) {
     Acc<KS> acc;
-    pm_mfma<KS, FDT>(M, fb, AT, LD, tid, acc);
+    pm_mfma<KS, FDT, B16, BSW>(M, fb, AT, LD, tid, acc);
     pp_epilogue<F32OUT, KS, FULL, FMT>(M.base, fb, acc, i0, gB, tid);
   }
 }
 
-template <bool F32OUT, int KS, int FDT, bool B16>
+// BSW: the B-fragment pair swap (launches of kSwapMinGrid workgroups and
+// more, 16-bit factors).
+template <bool F32OUT, int KS, int FDT, bool B16, bool BSW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_fused_pair_multi(JobTable tab) {
   extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
   const int tid = threadIdx.x;
   const uint32_t pair = xcd_remap(blockIdx.x, gridDim.x);
-  const PJM<KS> M = pjm_load<KS>(tab, pair);
+  const PJM<KS> M = pjm_load<KS, BSW>(tab, pair);
   const uint32_t p = pair - M.base.unit_begin;
   const uint32_t i0 = (p % M.base.bands_n) * kBandCols;
   const uint32_t gA = (p / M.base.bands_n) * (2 * kWavesPerGroup * kStripRows);
@@ -261,12 +334,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   // Base formats (ltxw_format): e4m3fn / e5m2, or with B16 bf16 / f16.
   constexpr int F0 = B16 ? 2 : 0, F1 = B16 ? 3 : 1;
   if (M.base.fmt == (uint32_t)F0) {
-    if (full) pair_units_multi<F32OUT, KS, F0, true, FDT>(M, AT, i0, gA, gB, hasB, tid);
-    else pair_units_multi<F32OUT, KS, F0, false, FDT>(M, AT, i0, gA, gB, hasB, tid);
+    if (full) pair_units_multi<F32OUT, KS, F0, true, FDT, BSW>(M, AT, i0, gA, gB, hasB, tid);
+    else pair_units_multi<F32OUT, KS, F0, false, FDT, BSW>(M, AT, i0, gA, gB, hasB, tid);
   } else {
-    if (full) pair_units_multi<F32OUT, KS, F1, true, FDT>(M, AT, i0, gA, gB, hasB, tid);
-    else pair_units_multi<F32OUT, KS, F1, false, FDT>(M, AT, i0, gA, gB, hasB, tid);
+    if (full) pair_units_multi<F32OUT, KS, F1, true, FDT, BSW>(M, AT, i0, gA, gB, hasB, tid);
+    else pair_units_multi<F32OUT, KS, F1, false, FDT, BSW>(M, AT, i0, gA, gB, hasB, tid);
   }
+}
+
+template <int KS, int FDT, bool B16>
+hipError_t launch_multi_ks(const JobTable& t, bool f32out, dim3 grid, size_t lds, hipStream_t stream) {
+  // The swap pairs K-steps of 16-bit factors; the host marks the pairs.
+  if constexpr (KS >= 2 && FactorRaw<FDT>::kBytes == 2) {
+    if (t.total_units >= kSwapMinGrid) {
+      if (f32out) hipLaunchKernelGGL((k_fused_pair_multi<true, KS, FDT, B16, true>), grid, dim3(256), lds, stream, t);
+      else hipLaunchKernelGGL((k_fused_pair_multi<false, KS, FDT, B16, true>), grid, dim3(256), lds, stream, t);
+      return hipGetLastError();
+    }
+  }
+  if (f32out) hipLaunchKernelGGL((k_fused_pair_multi<true, KS, FDT, B16, false>), grid, dim3(256), lds, stream, t);
+  else hipLaunchKernelGGL((k_fused_pair_multi<false, KS, FDT, B16, false>), grid, dim3(256), lds, stream, t);
+  return hipGetLastError();
 }
 
 template <int FDT, bool B16 = false>
@@ -274,23 +362,16 @@ hipError_t launch_multi_fdt(const JobTable& t, bool f32out, int ks, hipStream_t 
   if (t.total_units == 0) return hipSuccess;
   dim3 grid((unsigned)t.total_units);
   size_t lds = (size_t)kBandCols * (size_t)t.lds_ld * sizeof(uint16_t);
-#define LTXW_MULTI_LAUNCH(KS)                                                                            \
-  case KS:                                                                                               \
-    if (f32out) hipLaunchKernelGGL((k_fused_pair_multi<true, KS, FDT, B16>), grid, dim3(256), lds, stream, t); \
-    else hipLaunchKernelGGL((k_fused_pair_multi<false, KS, FDT, B16>), grid, dim3(256), lds, stream, t);       \
-    break;
   switch (ks) {
-    LTXW_MULTI_LAUNCH(1)
-    LTXW_MULTI_LAUNCH(2)
-    LTXW_MULTI_LAUNCH(3)
-    LTXW_MULTI_LAUNCH(4)
-    LTXW_MULTI_LAUNCH(5)
-    LTXW_MULTI_LAUNCH(6)
-    LTXW_MULTI_LAUNCH(7)
+    case 1: return launch_multi_ks<1, FDT, B16>(t, f32out, grid, lds, stream);
+    case 2: return launch_multi_ks<2, FDT, B16>(t, f32out, grid, lds, stream);
+    case 3: return launch_multi_ks<3, FDT, B16>(t, f32out, grid, lds, stream);
+    case 4: return launch_multi_ks<4, FDT, B16>(t, f32out, grid, lds, stream);
+    case 5: return launch_multi_ks<5, FDT, B16>(t, f32out, grid, lds, stream);
+    case 6: return launch_multi_ks<6, FDT, B16>(t, f32out, grid, lds, stream);
+    case 7: return launch_multi_ks<7, FDT, B16>(t, f32out, grid, lds, stream);
     default: return hipErrorInvalidValue;
   }
-#undef LTXW_MULTI_LAUNCH
-  return hipGetLastError();
 }
 
 }  // namespace

@@ -295,8 +295,19 @@ class Context:
                                           len(loras), out, out_dtype))
 
     def grouped(self, descs):
-        """descs: list of dicts with the TensorDesc fields; loras as (b, a, rank, coeff)."""
-        arr = (TensorDesc * max(1, len(descs)))()
+        """descs: list of dicts with the TensorDesc fields, loras as (b, a, rank,
+        coeff[, dtype]); or an array from make_descs (marshalled once, reusable)."""
+        if not isinstance(descs, ctypes.Array):
+            if not descs:
+                self._chk(lib().ltxw_dequant_lora_grouped(self.h, None, 0))
+                return
+            descs = self.make_descs(descs)
+        self._chk(lib().ltxw_dequant_lora_grouped(self.h, descs, len(descs)))
+
+    @staticmethod
+    def make_descs(descs):
+        """The ctypes TensorDesc array of a non-empty list of descriptor dicts."""
+        arr = (TensorDesc * len(descs))()
         for k, d in enumerate(descs):
             t = arr[k]
             t.w, t.out, t.scales = d["w"], d["out"], d.get("scales")
@@ -308,4 +319,4 @@ class Context:
             t.n_loras = len(loras)
             for l, x in enumerate(loras[:MAX_LORAS]):
                 t.loras[l] = Lora(*x)
-        self._chk(lib().ltxw_dequant_lora_grouped(self.h, arr, len(descs)))
+        return arr

@@ -165,6 +165,49 @@ def test_fused_non_bf16_factors(ctx, fdt, ranks, shape):
     assert np.array_equal(exact, U.oracle_bf16(case))
 
 
+@pytest.mark.parametrize("kind", ["r64", "r128", "r32+r128", "r64 f16 factors", "r64 bf16 base"])
+def test_large_launch_b_fragment_swap_bit_identical(ctx, kind):
+    """Launches of 3072 workgroups and more load the LoRA B fragments of a
+    K-step pair swapped on odd rows when a LoRA's row is a multiple of 128
+    bytes (ranks 64 and 128 here). Same data, same arithmetic: six copies of
+    one 4096 x 4096 tensor in one grouped launch (6 x 512 workgroups) equal the
+    tensor launched alone (512, no swap) bit for bit, and the tensor is within
+    the fused tolerance of the oracle on sampled rows."""
+    log("case: B-fragment swap", kind)
+    rows = cols = 4096
+    rng = np.random.default_rng(4096)
+    if kind == "r64 bf16 base":
+        case = {"w": synth.bf16_from_f64(rng.normal(0.0, 0.05, size=(rows, cols))), "scales": None, "rows": rows,
+                "cols": cols, "fmt": lw.FMT_BF16, "scale_mode": lw.SCALE_NONE, "loras": []}
+        b, a = synth.lora_factors(rng, rows, cols, 64)
+        case["loras"] = [(b, a, 64, 1.0)]
+    else:
+        ranks = {"r64": ((64, 1.0),), "r128": ((128, 0.5),), "r32+r128": ((32, 1.0), (128, 0.5)),
+                 "r64 f16 factors": ()}[kind]
+        case = synth.tensor_case(4097, rows, cols, synth.E4M3FN, synth.SCALE_ROW, loras=ranks)
+        if kind == "r64 f16 factors":
+            case["loras"] = [(factor_codes(rng, lw.FACTOR_F16, (rows, 64)), factor_codes(rng, lw.FACTOR_F16, (64, cols)),
+                              64, 1.0, lw.FACTOR_F16)]
+    d = U.Dev(ctx, case)
+    outs = []
+    try:
+        d.run()
+        alone = d.result()
+        sel = np.unique(np.concatenate([[0, 1, rows - 1], rng.choice(rows, 40, replace=False)]))
+        U.compare_lora_bf16(case, alone[sel], row_sel=sel)
+        outs = [ctx.alloc(rows * cols * 2) for _ in range(6)]
+        ctx.grouped([{"w": d.w, "out": o, "scales": d.s, "rows": rows, "cols": cols, "fmt": case["fmt"],
+                      "scale_mode": case["scale_mode"], "loras": d.loras} for o in outs])
+        for o in outs:
+            got = np.empty_like(alone)
+            ctx.download(o, got)
+            assert np.array_equal(got, alone)
+    finally:
+        for o in outs:
+            ctx.free(o)
+        d.free()
+
+
 def test_fused_f32_output(ctx):
     """f32 output (the reference's own HostTensor type): within the f32
     forward-error bound of both orders, 2*(rank+4)*2^-24*(|deq|+sum|cBA|)."""
