@@ -312,15 +312,23 @@ __global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
 }
 
 // Two vertically adjacent units of one band (rows [gA, gA + 256)).
-template <bool F32OUT, int KS, int FMT, bool FULL, bool BSW>
+// WFIRST (launches of at most kWFirstMaxGrid workgroups): the first unit's
+// FP8 bytes are requested before the factors.
+template <bool F32OUT, int KS, int FMT, bool FULL, bool BSW, bool WFIRST>
 __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i0, uint32_t gA, uint32_t gB,
                                            bool hasB, int tid) {
   constexpr int LD = 32 * KS + 8;
   Stage<KS> st;
-  pp_issue_a<KS>(J, i0, tid, st);
   Frag<KS> fa, fb;
-  pp_issue_f<KS, FULL, BSW>(J, i0, gA, tid, fa);
-  pp_issue_w<KS, FULL>(J, i0, gA, tid, fa);
+  if constexpr (WFIRST) {
+    pp_issue_w<KS, FULL>(J, i0, gA, tid, fa);
+    pp_issue_a<KS>(J, i0, tid, st);
+    pp_issue_f<KS, FULL, BSW>(J, i0, gA, tid, fa);
+  } else {
+    pp_issue_a<KS>(J, i0, tid, st);
+    pp_issue_f<KS, FULL, BSW>(J, i0, gA, tid, fa);
+    pp_issue_w<KS, FULL>(J, i0, gA, tid, fa);
+  }
   pp_issue_w<KS, FULL>(J, i0, hasB ? gB : gA, tid, fb);
   pp_stage<KS>(st, AT, LD, tid);
   __syncthreads();
@@ -341,8 +349,9 @@ __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i
 }
 
 // One workgroup per unit pair; the jobs' unit_begin count pairs. BSW: the
-// B-fragment pair swap (launches of kSwapMinGrid workgroups and more).
-template <bool F32OUT, int KS, bool BSW>
+// B-fragment pair swap (launches of kSwapMinGrid workgroups and more);
+// WFIRST: FP8 bytes before factors (launches of at most kWFirstMaxGrid).
+template <bool F32OUT, int KS, bool BSW, bool WFIRST>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 3 : 2))) void k_fused_pair(JobTable tab) {
   extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
   const int tid = threadIdx.x;
@@ -355,11 +364,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 3
   const bool hasB = gB < J.rows;
   const bool full = gB + kWavesPerGroup * kStripRows <= J.rows && i0 + kBandCols <= J.cols;
   if (J.fmt == 0) {
-    if (full) pair_units<F32OUT, KS, 0, true, BSW>(J, AT, i0, gA, gB, hasB, tid);
-    else pair_units<F32OUT, KS, 0, false, BSW>(J, AT, i0, gA, gB, hasB, tid);
+    if (full) pair_units<F32OUT, KS, 0, true, BSW, WFIRST>(J, AT, i0, gA, gB, hasB, tid);
+    else pair_units<F32OUT, KS, 0, false, BSW, WFIRST>(J, AT, i0, gA, gB, hasB, tid);
   } else {
-    if (full) pair_units<F32OUT, KS, 1, true, BSW>(J, AT, i0, gA, gB, hasB, tid);
-    else pair_units<F32OUT, KS, 1, false, BSW>(J, AT, i0, gA, gB, hasB, tid);
+    if (full) pair_units<F32OUT, KS, 1, true, BSW, WFIRST>(J, AT, i0, gA, gB, hasB, tid);
+    else pair_units<F32OUT, KS, 1, false, BSW, WFIRST>(J, AT, i0, gA, gB, hasB, tid);
   }
 }
 
@@ -522,19 +531,23 @@ hipError_t launch_dequant_tile(const DequantTileArgs& a, int fmt, int scale_mode
                   : dequant_tile_scale<1>(a, scale_mode, f32out, grid, stream);
 }
 
+template <int KS, bool BSW, bool WFIRST>
+hipError_t launch_fused_sched(const JobTable& t, bool f32out, dim3 grid, size_t lds, hipStream_t stream) {
+  if (f32out) hipLaunchKernelGGL((k_fused_pair<true, KS, BSW, WFIRST>), grid, dim3(256), lds, stream, t);
+  else hipLaunchKernelGGL((k_fused_pair<false, KS, BSW, WFIRST>), grid, dim3(256), lds, stream, t);
+  return hipGetLastError();
+}
+
 template <int KS>
 hipError_t launch_fused_ks(const JobTable& t, bool f32out, dim3 grid, size_t lds, hipStream_t stream) {
   // The swap pairs the K-steps of one LoRA: an even number of them.
   if constexpr (KS % 2 == 0) {
-    if (t.total_units >= kSwapMinGrid) {
-      if (f32out) hipLaunchKernelGGL((k_fused_pair<true, KS, true>), grid, dim3(256), lds, stream, t);
-      else hipLaunchKernelGGL((k_fused_pair<false, KS, true>), grid, dim3(256), lds, stream, t);
-      return hipGetLastError();
-    }
+    if (t.total_units >= kSwapMinGrid) return launch_fused_sched<KS, true, false>(t, f32out, grid, lds, stream);
   }
-  if (f32out) hipLaunchKernelGGL((k_fused_pair<true, KS, false>), grid, dim3(256), lds, stream, t);
-  else hipLaunchKernelGGL((k_fused_pair<false, KS, false>), grid, dim3(256), lds, stream, t);
-  return hipGetLastError();
+  if constexpr (KS <= 2) {
+    if (t.total_units <= kWFirstMaxGrid) return launch_fused_sched<KS, false, true>(t, f32out, grid, lds, stream);
+  }
+  return launch_fused_sched<KS, false, false>(t, f32out, grid, lds, stream);
 }
 
 hipError_t launch_fused(const JobTable& t, bool f32out, bool multi, int fdt, bool base16, hipStream_t stream) {
