@@ -31,7 +31,7 @@ struct ltxw_ctx {
     void* host = nullptr;
     void* dev = nullptr;
     size_t cap = 0;
-    hipEvent_t copied = nullptr;  // recorded after the slot's last upload
+    hipEvent_t copied = nullptr;  // recorded after the slot's last upload (last slot of a group only)
   };
   std::vector<TableSlot> tables;
   size_t next_table = 0;
