@@ -165,7 +165,7 @@ def test_fused_non_bf16_factors(ctx, fdt, ranks, shape):
     assert np.array_equal(exact, U.oracle_bf16(case))
 
 
-@pytest.mark.parametrize("kind", ["r64", "r128", "r32+r128", "r64 f16 factors", "r64 bf16 base"])
+@pytest.mark.parametrize("kind", ["r64", "r128", "r32+r128", "r64 f16 factors", "r64 bf16 base", "r128 f32 out"])
 def test_large_launch_b_fragment_swap_bit_identical(ctx, kind):
     """Launches of 3072 workgroups and more load the LoRA B fragments of a
     K-step pair swapped on odd rows when a LoRA's row is a multiple of 128
@@ -183,25 +183,33 @@ def test_large_launch_b_fragment_swap_bit_identical(ctx, kind):
         case["loras"] = [(b, a, 64, 1.0)]
     else:
         ranks = {"r64": ((64, 1.0),), "r128": ((128, 0.5),), "r32+r128": ((32, 1.0), (128, 0.5)),
-                 "r64 f16 factors": ()}[kind]
+                 "r64 f16 factors": (), "r128 f32 out": ((128, 0.5),)}[kind]
         case = synth.tensor_case(4097, rows, cols, synth.E4M3FN, synth.SCALE_ROW, loras=ranks)
         if kind == "r64 f16 factors":
             case["loras"] = [(factor_codes(rng, lw.FACTOR_F16, (rows, 64)), factor_codes(rng, lw.FACTOR_F16, (64, cols)),
                               64, 1.0, lw.FACTOR_F16)]
-    d = U.Dev(ctx, case)
+    out_dtype = lw.OUT_F32 if kind.endswith("f32 out") else lw.OUT_BF16
+    d = U.Dev(ctx, case, out_dtype)
     outs = []
     try:
         d.run()
         alone = d.result()
         sel = np.unique(np.concatenate([[0, 1, rows - 1], rng.choice(rows, 40, replace=False)]))
-        U.compare_lora_bf16(case, alone[sel], row_sel=sel)
-        outs = [ctx.alloc(rows * cols * 2) for _ in range(6)]
+        if out_dtype == lw.OUT_BF16:
+            U.compare_lora_bf16(case, alone[sel], row_sel=sel)
+        else:  # the f32 forward-error bound of both summation orders
+            import oracle_lib as O
+            w, f, m, sc, loras = U.oracle_args(case, sel)
+            bound = O.abs_bound_rows(w, f, m, sc, loras)
+            err = np.abs(alone[sel].astype(np.float64) - U.oracle_f32(case, sel).astype(np.float64))
+            assert np.all(err <= 2 * (128 + 4) * 2.0 ** -24 * bound)
+        outs = [ctx.alloc(rows * cols * d.ob) for _ in range(6)]
         ctx.grouped([{"w": d.w, "out": o, "scales": d.s, "rows": rows, "cols": cols, "fmt": case["fmt"],
-                      "scale_mode": case["scale_mode"], "loras": d.loras} for o in outs])
+                      "scale_mode": case["scale_mode"], "out_dtype": out_dtype, "loras": d.loras} for o in outs])
         for o in outs:
             got = np.empty_like(alone)
             ctx.download(o, got)
-            assert np.array_equal(got, alone)
+            assert np.array_equal(got.view(np.uint8), alone.view(np.uint8))
     finally:
         for o in outs:
             ctx.free(o)
