@@ -101,12 +101,13 @@ def read_traffic(workload):
     return vals.get("traffic")
 
 
-def cpu_baseline(case, budget_s):
-    """The oracle on the same tensor, all host threads, repeated to ~budget_s."""
+def cpu_baseline(case, budget_s, threads=None):
+    """The oracle on the same tensor, `threads` host threads (default all, at
+    most 16), repeated to ~budget_s."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = threads or min(16, os.cpu_count() or 1)
     loras = [(b, a, O.BF16, c) for (b, a, r, c) in case["loras"]]
     fmt = O.E4M3FN if case["fmt"] == 0 else O.E5M2
     args = (case["w"], fmt, case["scale_mode"], case["scales"], loras)
@@ -475,6 +476,10 @@ def main():
                "sample": f"{reps} x the {c0['rows']}x{c0['cols']} tensor through the C oracle "
                          f"(reference operation order), {threads} threads, {dt:.1f} s",
                "s_per_tensor": round(dt / reps, 4)}
+        # One thread, as the reference runs (a scalar loop on one thread).
+        _, reps1, dt1 = cpu_baseline(c0, min(5.0, args.cpu_seconds / 2), threads=1)
+        cpu["value_1_thread"] = round(b0 * reps1 / dt1 / 1e9, 3)
+        cpu["s_per_tensor_1_thread"] = round(dt1 / reps1, 4)
 
     for p in allocs:
         ctx.free(p)
