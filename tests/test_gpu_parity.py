@@ -165,16 +165,19 @@ def test_fused_non_bf16_factors(ctx, fdt, ranks, shape):
     assert np.array_equal(exact, U.oracle_bf16(case))
 
 
-@pytest.mark.parametrize("kind", ["r64", "r128", "r32+r128", "r64 f16 factors", "r64 bf16 base", "r128 f32 out"])
+@pytest.mark.parametrize("kind", ["r64", "r128", "r32+r128", "r64 f16 factors", "r64 bf16 base", "r128 f32 out",
+                                  "r128 ragged", "r32+r128 ragged"])
 def test_large_launch_b_fragment_swap_bit_identical(ctx, kind):
     """Launches of 3072 workgroups and more load the LoRA B fragments of a
     K-step pair swapped on odd rows when a LoRA's row is a multiple of 128
     bytes (ranks 64 and 128 here). Same data, same arithmetic: six copies of
     one 4096 x 4096 tensor in one grouped launch (6 x 512 workgroups) equal the
     tensor launched alone (512, no swap) bit for bit, and the tensor is within
-    the fused tolerance of the oracle on sampled rows."""
+    the fused tolerance of the oracle on sampled rows. The ragged kinds take
+    4104 x 4104 (6 x 561 workgroups, partial tiles at the row and column ends)."""
     log("case: B-fragment swap", kind)
-    rows = cols = 4096
+    rows = cols = 4104 if kind.endswith("ragged") else 4096
+    kind = kind.replace(" ragged", "")
     rng = np.random.default_rng(4096)
     if kind == "r64 bf16 base":
         case = {"w": synth.bf16_from_f64(rng.normal(0.0, 0.05, size=(rows, cols))), "scales": None, "rows": rows,
