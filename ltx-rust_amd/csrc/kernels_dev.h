@@ -170,7 +170,8 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t n) {
 // Issue order is latency order: the L2-resident factor loads (A for the LDS
 // stage, then every B fragment) go out first, the FP8 bytes and scales from
 // HBM last. Loads retire in order, so staging, the barrier and the MFMAs run
-// while the HBM data is still in flight.
+// while the HBM data is still in flight. (Single-LoRA launches of at most
+// kWFirstMaxGrid workgroups request the first unit's FP8 bytes first.)
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void load_job(const JobTable& t, uint64_t unit, JobDev& J) {
   if (t.n_jobs == 1) {
