@@ -256,6 +256,49 @@ def test_fused_nan_inf_codes(ctx):
     U.compare_lora_bf16(case, got)
 
 
+def test_many_grouped_calls_in_flight(ctx):
+    """48 grouped calls queued without a wait, each with its own outputs: the
+    host runs ahead of the GPU through the ring of job-table slots, so every
+    slot's host copy and device table is reused while earlier calls are still
+    queued. Every output must equal the tensor's own single-call result, and
+    an empty grouped call is a no-op."""
+    log("case: grouped calls in flight")
+    cases = [synth.tensor_case(4800 + k, 4096, 4096, synth.E4M3FN, synth.SCALE_ROW, loras=((64, 1.0),))
+             for k in range(2)]
+    devs = [U.Dev(ctx, c) for c in cases]
+    outs = []
+    try:
+        singles = []
+        for d in devs:
+            d.run()
+            singles.append(d.result())
+        n_calls = 48
+        outs = [[ctx.alloc(d.n * d.ob) for d in devs] for _ in range(n_calls)]
+        for call in outs:
+            for o, d in zip(call, devs):
+                ctx.memset(o, 0xFF, d.n * d.ob)
+        ctx.synchronize()
+        descs = [lw.Context.make_descs([{"w": d.w, "out": o, "scales": d.s, "rows": d.case["rows"],
+                                         "cols": d.case["cols"], "fmt": d.case["fmt"],
+                                         "scale_mode": d.case["scale_mode"], "loras": d.loras}
+                                        for o, d in zip(call, devs)]) for call in outs]
+        for arr in descs:
+            ctx.grouped(arr)
+        ctx.grouped([])
+        ctx.synchronize()
+        for k, call in enumerate(outs):
+            for o, d, s in zip(call, devs, singles):
+                got = np.empty_like(s)
+                ctx.download(o, got)
+                assert np.array_equal(got, s), "call %d" % k
+    finally:
+        for call in outs:
+            for o in call:
+                ctx.free(o)
+        for d in devs:
+            d.free()
+
+
 def test_grouped_block_matches_single_calls(ctx):
     """A grouped launch over mixed tensors equals per-tensor calls bit for bit."""
     log("case: grouped vs single")
