@@ -345,9 +345,14 @@ int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool 
     memcpy(slot->host, jobs.data(), jb);
     int64_t* begins = reinterpret_cast<int64_t*>((char*)slot->host + off_b);
     for (size_t k = 0; k < jobs.size(); ++k) begins[k] = jobs[k].unit_begin;
-    HIP_TRY(ctx, hipMemcpyAsync(slot->dev, slot->host, off_b + bb, hipMemcpyHostToDevice, ctx->compute),
-            "job table upload");
-    if (record) HIP_TRY(ctx, hipEventRecord(slot->copied, ctx->compute), "job table event");
+    hipError_t e = hipMemcpyAsync(slot->dev, slot->host, off_b + bb, hipMemcpyHostToDevice, ctx->compute);
+    if (e == hipSuccess && record) e = hipEventRecord(slot->copied, ctx->compute);
+    if (e != hipSuccess) {
+      // The group's event may now be missing for this round: drain the stream
+      // so that no queued upload still reads a host slot the next round rewrites.
+      (void)hipStreamSynchronize(ctx->compute);
+      return hip_fail(ctx, e, "job table upload");
+    }
     t.jobs = reinterpret_cast<const ltxw::JobDev*>(slot->dev);
     t.begins = reinterpret_cast<const int64_t*>((char*)slot->dev + off_b);
   }
