@@ -219,6 +219,43 @@ def test_large_launch_b_fragment_swap_bit_identical(ctx, kind):
         d.free()
 
 
+@pytest.mark.parametrize("ranks", [((64, 1.0),), ((32, 1.0), (128, 0.5))])
+@pytest.mark.parametrize("copies", [1, 6])
+def test_zero_lora_equals_dequant_at_full_size(ctx, ranks, copies):
+    """A size-independent property at the full 4096 x 4096 size: with every B
+    factor zero the LoRA product is +0, and the fused epilogue
+    fma(scale, decode(w), coeff * 0) is the dequantisation fma(scale, decode(w), 0)
+    bit for bit (row scales, so -0 turns +0 on both sides). Covers every
+    element's index mapping in the fused kernels' epilogue; six copies in one
+    grouped launch take the B-fragment pair swap."""
+    log("case: zero LoRA", ranks, copies)
+    case = synth.tensor_case(4444, 4096, 4096, synth.E4M3FN, synth.SCALE_ROW, loras=ranks)
+    case["loras"] = [(np.zeros_like(b), a, r, c) for (b, a, r, c) in case["loras"]]
+    d = U.Dev(ctx, case)
+    outs = []
+    try:
+        if copies == 1:
+            d.run()
+            got = [d.result()]
+        else:
+            outs = [ctx.alloc(d.n * d.ob) for _ in range(copies)]
+            ctx.grouped([{"w": d.w, "out": o, "scales": d.s, "rows": 4096, "cols": 4096, "fmt": case["fmt"],
+                          "scale_mode": case["scale_mode"], "loras": d.loras} for o in outs])
+            got = []
+            for o in outs:
+                g = np.empty((4096, 4096), np.uint16)
+                ctx.download(o, g)
+                got.append(g)
+        ctx.dequant(d.w, 4096, 4096, case["fmt"], case["scale_mode"], d.s, d.out)
+        deq = d.result()
+        for g in got:
+            assert np.array_equal(g, deq)
+    finally:
+        for o in outs:
+            ctx.free(o)
+        d.free()
+
+
 def test_fused_f32_output(ctx):
     """f32 output (the reference's own HostTensor type): within the f32
     forward-error bound of both orders, 2*(rank+4)*2^-24*(|deq|+sum|cBA|)."""
