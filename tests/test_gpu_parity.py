@@ -256,6 +256,27 @@ def test_zero_lora_equals_dequant_at_full_size(ctx, ranks, copies):
         d.free()
 
 
+@pytest.mark.parametrize("ranks", [((64, 1.0),), ((32, 1.0), (128, 0.5))])
+def test_row_and_column_permutation_equivariance(ctx, ranks):
+    """Rows and columns are independent and every element's sum runs in the
+    same order wherever it sits, so permuting the rows of W, the scales and B
+    (or the columns of W and A) permutes the output the same way, bit for bit,
+    at the full 4096 x 4104 size (a partial column band included). Catches a
+    factor row or column paired with the wrong output."""
+    log("case: permutation", ranks)
+    rows, cols = 4096, 4104
+    case = synth.tensor_case(4545, rows, cols, synth.E4M3FN, synth.SCALE_ROW, loras=ranks)
+    rng = np.random.default_rng(45)
+    p, q = rng.permutation(rows), rng.permutation(cols)
+    base = run_case(ctx, case)
+    by_rows = dict(case, w=np.ascontiguousarray(case["w"][p]), scales=np.ascontiguousarray(case["scales"][p]),
+                   loras=[(np.ascontiguousarray(b[p]), a, r, c) for (b, a, r, c) in case["loras"]])
+    assert np.array_equal(run_case(ctx, by_rows), base[p])
+    by_cols = dict(case, w=np.ascontiguousarray(case["w"][:, q]),
+                   loras=[(b, np.ascontiguousarray(a[:, q]), r, c) for (b, a, r, c) in case["loras"]])
+    assert np.array_equal(run_case(ctx, by_cols), base[:, q])
+
+
 def test_fused_f32_output(ctx):
     """f32 output (the reference's own HostTensor type): within the f32
     forward-error bound of both orders, 2*(rank+4)*2^-24*(|deq|+sum|cBA|)."""
