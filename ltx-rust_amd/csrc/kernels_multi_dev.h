@@ -133,7 +133,9 @@ __device__ __forceinline__ void pm_issue_a(const PJM<KS>& M, uint32_t i0, int ti
   constexpr uint32_t E = FactorRaw<FDT>::kBytes;
   const int sq = tid & 15;
   const uint32_t cols = M.base.cols;
-  const uint32_t scol = i0 + 8 * (tid >> 4);
+  // Column groups as in pp_issue_a; a group is 8 E bytes wide, so the partner
+  // group in the other half of a 128-byte line is 64 / (8 E) groups away.
+  const uint32_t scol = i0 + 8 * a_group(tid, 8 / E);
   const bool scol_ok = scol < cols;
   const uint32_t k = 2 * sq;
 #pragma unroll
@@ -155,7 +157,8 @@ __device__ __forceinline__ void pm_stage(const StageM<KS, FDT>& st, uint16_t* AT
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) {
       const uint32_t pair = __builtin_amdgcn_perm(hi[jj >> 1], lo[jj >> 1], (jj & 1) ? 0x07060302u : 0x05040100u);
-      *reinterpret_cast<uint32_t*>(&AT[(jj * 16 + (tid >> 4)) * ld + 32 * t + 2 * sq]) = pair;
+      *reinterpret_cast<uint32_t*>(&AT[(jj * 16 + a_group(tid, 8 / FactorRaw<FDT>::kBytes)) * ld + 32 * t + 2 * sq]) =
+          pair;
     }
   }
 }
