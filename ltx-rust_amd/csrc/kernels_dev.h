@@ -130,10 +130,11 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* G(T* p) {
 // 12.5 -> 11.9 us), while the remap wins from about a DiT block up.
 constexpr uint32_t kRemapMinGrid = 2048;
 // Launches of at least this many workgroups use the B-fragment pair swap
-// (BSW, below): measured 1-3% faster per DiT block at rank 64 and 5-7% at
-// rank 128, against 0.3-1 us slower on one 4096 x 4096 layer (512
-// workgroups) and no gain at 2048.
-constexpr int64_t kSwapMinGrid = 3072;
+// (BSW, below): measured 2% faster on two 4096 x 4096 layers (1024
+// workgroups), 1.5-2% on four layers or an FFN matrix (2048), 1-3% per DiT
+// block at rank 64 and 5-7% at rank 128, against 0.1-1 us slower on one
+// layer (512 workgroups, all resident at once).
+constexpr int64_t kSwapMinGrid = 1024;
 // Single-LoRA launches of at most this many workgroups (two per CU: every
 // workgroup starts at once) request the first unit's FP8 bytes before the
 // factors: one 4096 x 4096 layer 11.8-12.2 -> 11.7-11.8 us; from four layers

@@ -168,7 +168,7 @@ def test_fused_non_bf16_factors(ctx, fdt, ranks, shape):
 @pytest.mark.parametrize("kind", ["r64", "r128", "r32+r128", "r64 f16 factors", "r64 bf16 base", "r128 f32 out",
                                   "r128 ragged", "r32+r128 ragged"])
 def test_large_launch_b_fragment_swap_bit_identical(ctx, kind):
-    """Launches of 3072 workgroups and more load the LoRA B fragments of a
+    """Launches of 1024 workgroups and more load the LoRA B fragments of a
     K-step pair swapped on odd rows when a LoRA's row is a multiple of 128
     bytes (ranks 64 and 128 here). Same data, same arithmetic: six copies of
     one 4096 x 4096 tensor in one grouped launch (6 x 512 workgroups) equal the
