@@ -136,9 +136,12 @@ int ltxw_alloc(ltxw_ctx* ctx, size_t bytes, void** dptr);
 int ltxw_free(ltxw_ctx* ctx, void* dptr);
 int ltxw_memset(ltxw_ctx* ctx, void* dptr, int value, size_t bytes);
 
-/* Host -> device copy staged through the pinned ring on the copy stream; the
- * compute stream waits for it, so later operations see the data. The host
- * buffer may be reused as soon as the call returns (it has been staged).
+/* Host -> device copy staged through the pinned ring on the copy stream, in
+ * call order: it starts after every operation queued on the context before
+ * it (so a device buffer may be refilled while a kernel that reads it is
+ * still queued), and the compute stream waits for it, so later operations
+ * see the data. The host buffer may be reused as soon as the call returns
+ * (it has been staged).
  * Replaces `Entry::read_raw`'s `to_vec` copy (src/store.rs:45-78). */
 int ltxw_upload(ltxw_ctx* ctx, const void* host_src, size_t bytes, void* dst);
 

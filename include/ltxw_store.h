@@ -127,15 +127,23 @@ void ltxw_report_free(ltxw_merge_report* r);
 int ltxw_store_n_deltas(const ltxw_store* s, const char* key);
 int ltxw_store_delta(const ltxw_store* s, const char* key, int index, int32_t* rank, float* coeff);
 
-/* Scale policy of materialise / read. Default: a `{key}_scale` with exactly
- * shape[0] elements (shape[0] > 1, two or more dims) scales row o by
- * element o; any other scale tensor scales everything by its element 0, as
- * the reference does for all (src/store.rs:498-508, :732-735; empty: 1.0).
- * LTXW_MAT_SCALE_FIRST applies the reference's element-0 rule to all. */
+/* Options of ltxw_store_materialize and ltxw_store_read. The two entry
+ * points differ in their defaults:
+ *   materialize: a `{key}_scale` with exactly shape[0] elements (shape[0] > 1,
+ *     two or more dims) scales row o by element o (an extension: per-output-
+ *     channel FP8 scales), any other scale tensor by its element 0; LoRA deltas
+ *     go through the MFMA kernels where they take them (within 1 bf16 ulp of
+ *     the reference's result).
+ *   read: the reference's `read` exactly: every scale tensor scales by its
+ *     element 0 (src/store.rs:498-508, :732-735; empty: 1.0) and the deltas run
+ *     in the reference's operation order, so the f32 result is bit-identical.
+ * LTXW_MAT_SCALE_FIRST / LTXW_MAT_EXACT select the reference's rules (no-ops
+ * for read); LTXW_MAT_ROW_SCALES / LTXW_MAT_MFMA select the extensions (no-ops
+ * for materialize). A rule and its opposite together are LTXW_ERR_INVALID_ARG. */
 #define LTXW_MAT_SCALE_FIRST 1u
-/* Bit-identical LoRA merges: every key with deltas in the reference's
- * operation order (LTXW_DESC_EXACT). */
 #define LTXW_MAT_EXACT 2u
+#define LTXW_MAT_ROW_SCALES 4u
+#define LTXW_MAT_MFMA 8u
 
 /* Materialise tensors into caller-allocated device buffers: outs[k] holds
  * numel(keys[k]) elements of out_dtype (ltxw_out_dtype) in row-major order.
@@ -144,8 +152,10 @@ int ltxw_store_delta(const ltxw_store* s, const char* key, int index, int32_t* r
  * bf16 (RNE) or kept f32. Non-FP8 base tensors and >= 2-D shapes are
  * accepted; a key with deltas must be [out, in] (src/store.rs:767-779).
  * LoRA factors of every type `merge_lora` accepts are taken (bf16 on the
- * MFMA path, the others in the reference's order); at most LTXW_MAX_LORAS
- * deltas per key.
+ * MFMA path, the others in the reference's order). A key merged with more
+ * than LTXW_MAX_LORAS deltas runs all of them in the reference's order, in
+ * passes of up to LTXW_MAX_LORAS deltas through an f32 accumulator (for bf16
+ * output a device scratch buffer of 4 bytes per element, kept by the context).
  *
  * Bytes go mapped file -> pinned ring (ctx host threads) -> HBM on the copy
  * stream, batch by batch through a device ring, and each batch is
@@ -157,7 +167,10 @@ int ltxw_store_materialize(ltxw_store* s, ltxw_ctx* ctx, const char* const* keys
                            int32_t out_dtype, uint32_t flags, void* const* outs);
 
 /* `WeightStore::read` (src/store.rs:479-521) on the device: the f32 tensor
- * into host memory (n == numel). Synchronous. */
+ * into host memory (n == numel), bit-identical to the reference's (element-0
+ * scale rule, every merged delta in merge order and in the reference's
+ * operation order). `flags` (LTXW_MAT_ROW_SCALES, LTXW_MAT_MFMA) opt into the
+ * materialize extensions. Synchronous. */
 int ltxw_store_read(ltxw_store* s, ltxw_ctx* ctx, const char* key, uint32_t flags, float* out, int64_t n);
 
 #ifdef __cplusplus

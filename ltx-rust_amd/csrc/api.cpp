@@ -245,6 +245,7 @@ int run_exact(ltxw_ctx* ctx, const ltxw_tensor_desc& d, const ltxw::DescEx* ex) 
     a.plain_scale = ex->plain_scale;
     a.has_post = ex->has_post;
     a.post_mul = ex->post_mul;
+    a.canon_nan = ex->canon_nan;
   }
   a.bands_n = (uint32_t)((d.cols + ltxw::kExactCols - 1) / ltxw::kExactCols);
   HIP_TRY(ctx, ltxw::launch_exact(a, d.out_dtype == LTXW_OUT_F32, ctx->compute), "exact kernel launch");
@@ -382,7 +383,7 @@ int ltxw::run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n, const D
     uint64_t cnt = counts[(size_t)k];
     if (cnt == 0) continue;
     int rc = LTXW_OK;
-    const bool extras = ex && (ex[k].plain_scale || ex[k].has_post);
+    const bool extras = ex && (ex[k].plain_scale || ex[k].has_post || ex[k].canon_nan);
     if (extras || (d.n_loras > 0 && ((d.flags & LTXW_DESC_EXACT) || !fused_ok(d)))) {
       rc = run_exact(ctx, d, extras ? &ex[k] : nullptr);
     } else if (d.n_loras == 0) {
@@ -464,6 +465,8 @@ int ltxw_ctx_create(int device, size_t staging_bytes, int n_staging, ltxw_ctx** 
     return bail(LTXW_ERR_HIP, "compute stream", e);
   if ((e = hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking)) != hipSuccess)
     return bail(LTXW_ERR_HIP, "copy stream", e);
+  if ((e = hipEventCreateWithFlags(&c->compute_mark, hipEventDisableTiming)) != hipSuccess)
+    return bail(LTXW_ERR_HIP, "event", e);
   c->tables.resize(2 * kTableGroup);
   for (auto& t : c->tables)
     if ((e = hipEventCreateWithFlags(&t.copied, hipEventDisableTiming)) != hipSuccess)
@@ -480,6 +483,7 @@ void ltxw_ctx_destroy(ltxw_ctx* ctx) {
   if (ctx->stage_block) (void)hipHostFree(ctx->stage_block);
   for (hipEvent_t ev : ctx->stage_done) (void)hipEventDestroy(ev);
   for (void* p : ctx->ring) (void)hipFree(p);
+  if (ctx->tmp) (void)hipFree(ctx->tmp);
   for (hipEvent_t ev : ctx->ring_free) (void)hipEventDestroy(ev);
   for (hipEvent_t ev : ctx->ring_ready) (void)hipEventDestroy(ev);
   for (auto& t : ctx->tables) {
@@ -487,6 +491,7 @@ void ltxw_ctx_destroy(ltxw_ctx* ctx) {
     if (t.dev) (void)hipFree(t.dev);
     if (t.copied) (void)hipEventDestroy(t.copied);
   }
+  if (ctx->compute_mark) (void)hipEventDestroy(ctx->compute_mark);
   if (ctx->compute) (void)hipStreamDestroy(ctx->compute);
   if (ctx->copy) (void)hipStreamDestroy(ctx->copy);
   delete ctx;
@@ -543,6 +548,11 @@ int ltxw_upload(ltxw_ctx* ctx, const void* host_src, size_t bytes, void* dst) {
   if (int rc = check_extent(ctx, dst, bytes, "upload destination")) return rc;
   HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
   if (int rc = ltxw::ensure_staging(ctx)) return rc;
+  // Call order: the copy must not overtake kernels or memsets already queued
+  // on the compute stream that read or write `dst` (a buffer reused for the
+  // next tensor while the previous one's kernel is still queued).
+  HIP_TRY(ctx, hipEventRecord(ctx->compute_mark, ctx->compute), "upload ordering event");
+  HIP_TRY(ctx, hipStreamWaitEvent(ctx->copy, ctx->compute_mark, 0), "copy waits for queued work");
   const char* src = (const char*)host_src;
   size_t done = 0;
   while (done < bytes) {

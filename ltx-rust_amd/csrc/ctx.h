@@ -15,6 +15,9 @@ struct ltxw_ctx {
   int host_threads = 8;
   hipStream_t compute = nullptr;
   hipStream_t copy = nullptr;
+  // Recorded on the compute stream at each upload, which the copy stream
+  // waits for: an upload lands after every operation queued before it.
+  hipEvent_t compute_mark = nullptr;
   // Pinned staging ring for host -> device uploads (allocated on first use):
   // n_stage slots of stage_bytes, consecutive in one block. Slot k may be
   // refilled once stage_done[k] (recorded on the copy stream after the
@@ -42,6 +45,10 @@ struct ltxw_ctx {
   std::vector<void*> ring;
   std::vector<hipEvent_t> ring_free, ring_ready;
   size_t ring_bytes = 0;
+  // Device scratch of the store: the f32 accumulator of keys merged with
+  // more LoRAs than one launch takes (grown on demand).
+  void* tmp = nullptr;
+  size_t tmp_bytes = 0;
   std::string err;
 };
 
@@ -53,12 +60,17 @@ int fail(ltxw_ctx* ctx, int code, const char* fmt, ...) __attribute__((format(pr
 // Allocates the pinned staging ring if it is not there yet.
 int ensure_staging(ltxw_ctx* ctx);
 
-// Per-descriptor extras of the store's open-time gate fold: scale as a plain
-// multiply, then a multiply by `post_mul` (before the LoRA deltas).
+// Per-descriptor extras of the store: the open-time gate fold (scale as a
+// plain multiply, then a multiply by `post_mul`, before the LoRA deltas) and
+// the NaN rule of chained passes. Descriptors with extras take the
+// reference-order kernel.
 struct DescEx {
   int32_t plain_scale = 0;
   int32_t has_post = 0;
   float post_mul = 1.0f;
+  // Canonicalise NaN results as for an FP8 source (a later pass of a chain
+  // whose first pass read FP8 bytes).
+  int32_t canon_nan = 0;
 };
 
 // Validates and queues the descriptors on the compute stream (the body of

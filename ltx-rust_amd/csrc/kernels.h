@@ -106,6 +106,7 @@ struct ExactArgs {
   int32_t has_post;
   float post_mul;
   uint32_t bands_n;     // ceil(cols / kExactCols)
+  int32_t canon_nan;    // canonicalise NaN results whatever the base format
 };
 constexpr int kExactCols = 128;
 constexpr int kExactRows = 64;

@@ -277,7 +277,7 @@ __global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
   for (int k = 0; k < 4; ++k) {
     const uint64_t o = g0 + rs + 16 * k;
     if (o >= rows) continue;
-    if (J.fmt <= 1) canon_nan_wave<8>(acc[k]);
+    if (J.fmt <= 1 || g.canon_nan) canon_nan_wave<8>(acc[k]);
     if (o_vec) {
       if (F32OUT) {
         f32x4* dst = reinterpret_cast<f32x4*>(reinterpret_cast<float*>(J.out) + o * cols + c0);

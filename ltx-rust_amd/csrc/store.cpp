@@ -371,12 +371,12 @@ struct Plan {
   int scale_mode;
   std::vector<float> scales;
   std::vector<const Delta*> deltas;
-  const uint8_t* fb[LTXW_MAX_LORAS];  // mapped factor bytes
-  const uint8_t* fa[LTXW_MAX_LORAS];
-  int fdt[LTXW_MAX_LORAS];            // ltxw_factor_dtype
-  ltxw::DescEx ex;                    // gate-fold extras
+  std::vector<const uint8_t*> fb, fa;  // mapped factor bytes, per delta
+  std::vector<int> fdt;                // ltxw_factor_dtype, per delta
+  ltxw::DescEx ex;                     // gate-fold extras
   // Offsets inside the batch's device slot.
-  uint64_t off_w, off_s, off_b[LTXW_MAX_LORAS], off_a[LTXW_MAX_LORAS], bytes;
+  uint64_t off_w, off_s, bytes;
+  std::vector<uint64_t> off_b, off_a;
 };
 
 const uint8_t* entry_bytes(const ltxw_store* s, const Entry& e);
@@ -439,9 +439,6 @@ int make_plan(const ltxw_store* s, const std::string& key, uint32_t flags, int o
   // Merged deltas (store.rs:510-515, add_to's checks at :767-779).
   auto dl = s->deltas.find(key);
   if (dl != s->deltas.end()) {
-    if (dl->second.size() > (size_t)LTXW_MAX_LORAS)
-      return sfail(LTXW_ERR_UNSUPPORTED, "key \"%s\" has %zu merged LoRAs; the device path takes at most %d",
-                   key.c_str(), dl->second.size(), LTXW_MAX_LORAS);
     for (const Delta& d : dl->second) {
       const uint64_t out_in = d.out * d.in;
       if ((d.in && out_in / d.in != d.out) || out_in != p->numel || d.in == 0 || d.rank == 0)
@@ -454,10 +451,9 @@ int make_plan(const ltxw_store* s, const std::string& key, uint32_t flags, int o
       if (d.rank > (1u << 20))
         return sfail(LTXW_ERR_UNSUPPORTED, "LoRA rank %llu of \"%s\" is too large", (unsigned long long)d.rank,
                      key.c_str());
-      const size_t l = p->deltas.size();
-      p->fb[l] = d.lora->file->base + tb.begin;
-      p->fa[l] = d.lora->file->base + ta.begin;
-      p->fdt[l] = factor_dtype(ta.dtype);
+      p->fb.push_back(d.lora->file->base + tb.begin);
+      p->fa.push_back(d.lora->file->base + ta.begin);
+      p->fdt.push_back(factor_dtype(ta.dtype));
       p->deltas.push_back(&d);
     }
     if (!p->deltas.empty()) {
@@ -472,6 +468,8 @@ int make_plan(const ltxw_store* s, const std::string& key, uint32_t flags, int o
   off = align_up(off + p->numel * (uint64_t)p->esize);
   p->off_s = off;
   off = align_up(off + 4 * (uint64_t)p->scales.size());
+  p->off_b.resize(p->deltas.size());
+  p->off_a.resize(p->deltas.size());
   for (size_t l = 0; l < p->deltas.size(); ++l) {
     const Delta& d = *p->deltas[l];
     const uint64_t fs = factor_size(p->fdt[l]);
@@ -548,6 +546,27 @@ int ensure_ring(ltxw_ctx* ctx, uint64_t need) {
   return LTXW_OK;
 }
 
+// Grows the context's device scratch (the chained passes' f32 accumulator)
+// to `need` bytes; work already queued may still use the old buffer.
+int ensure_tmp(ltxw_ctx* ctx, uint64_t need) {
+  if (need <= ctx->tmp_bytes) return LTXW_OK;
+  hipError_t he;
+  if (ctx->tmp) {
+    if ((he = hipStreamSynchronize(ctx->compute)) != hipSuccess)
+      return sfail(LTXW_ERR_HIP, "scratch resize: %s", hipGetErrorString(he));
+    (void)hipFree(ctx->tmp);
+    ctx->tmp = nullptr;
+    ctx->tmp_bytes = 0;
+  }
+  if (hipMalloc(&ctx->tmp, need) != hipSuccess) {
+    (void)hipGetLastError();
+    ctx->tmp = nullptr;
+    return sfail(LTXW_ERR_OOM, "device scratch of %llu bytes", (unsigned long long)need);
+  }
+  ctx->tmp_bytes = need;
+  return LTXW_OK;
+}
+
 // Host copy granularity: a staging slot is filled in sub-chunks of this size
 // by whichever host threads are free, so one slot fills at the threads'
 // combined rate.
@@ -573,6 +592,13 @@ int run_pipeline(ltxw_ctx* ctx, std::vector<Plan>& plans, int out_dtype, uint32_
   uint64_t need = 512ull << 20;
   for (const Plan& p : plans) need = std::max(need, p.bytes);
   if (int rc = ensure_ring(ctx, need)) return rc;
+  // f32 accumulator of keys with more than LTXW_MAX_LORAS deltas and bf16
+  // output (their passes run in stream order, so one buffer serves all).
+  uint64_t tmp_need = 0;
+  if (out_dtype == LTXW_OUT_BF16)
+    for (const Plan& p : plans)
+      if (p.deltas.size() > (size_t)LTXW_MAX_LORAS) tmp_need = std::max(tmp_need, 4 * p.numel);
+  if (int rc = ensure_tmp(ctx, tmp_need)) return rc;
   const uint64_t stage = ctx->stage_bytes;
   const size_t S = ctx->stage.size(), R = ctx->ring.size();
 
@@ -739,22 +765,38 @@ int run_pipeline(ltxw_ctx* ctx, std::vector<Plan>& plans, int out_dtype, uint32_
     exs.clear();
     for (size_t k = b.first_plan; k < b.first_plan + b.n_plans; ++k) {
       const Plan& p = plans[k];
-      ltxw_tensor_desc d{};
-      d.w = (const uint8_t*)(base + p.off_w);
-      d.out = p.out;
-      d.scales = p.scales.empty() ? nullptr : (const float*)(base + p.off_s);
-      d.rows = (int64_t)p.rows;
-      d.cols = (int64_t)p.cols;
-      d.fmt = p.fmt;
-      d.scale_mode = p.scale_mode;
-      d.out_dtype = out_dtype;
-      d.n_loras = (int32_t)p.deltas.size();
-      d.flags = (flags & LTXW_MAT_EXACT) ? LTXW_DESC_EXACT : 0;
-      for (size_t l = 0; l < p.deltas.size(); ++l)
-        d.loras[l] = {base + p.off_b[l], base + p.off_a[l], (int32_t)p.deltas[l]->rank, p.deltas[l]->coeff,
-                      p.fdt[l], 0};
-      descs.push_back(d);
-      exs.push_back(p.ex);
+      const size_t nd = p.deltas.size();
+      // Up to LTXW_MAX_LORAS deltas: one descriptor. More: passes of up to
+      // LTXW_MAX_LORAS deltas each, in merge order and in the reference's
+      // operation order, through an f32 accumulator (the output itself for
+      // f32, else the context's scratch): each pass continues the previous
+      // pass's per-element FMA chain, so the result equals one long chain
+      // (store.rs:510-515).
+      const bool chained = nd > (size_t)LTXW_MAX_LORAS;
+      void* acc = out_dtype == LTXW_OUT_F32 ? p.out : ctx->tmp;
+      for (size_t l0 = 0; l0 == 0 || l0 < nd; l0 += LTXW_MAX_LORAS) {
+        const size_t l1 = std::min(nd, l0 + (size_t)LTXW_MAX_LORAS);
+        const bool first = l0 == 0, last = l1 == nd;
+        ltxw_tensor_desc d{};
+        d.w = first ? (const uint8_t*)(base + p.off_w) : (const uint8_t*)acc;
+        d.out = last ? p.out : acc;
+        d.scales = (first && !p.scales.empty()) ? (const float*)(base + p.off_s) : nullptr;
+        d.rows = (int64_t)p.rows;
+        d.cols = (int64_t)p.cols;
+        d.fmt = first ? p.fmt : LTXW_FMT_F32;
+        d.scale_mode = first ? p.scale_mode : LTXW_SCALE_NONE;
+        d.out_dtype = last ? out_dtype : LTXW_OUT_F32;
+        d.n_loras = (int32_t)(l1 - l0);
+        d.flags = (chained || (flags & LTXW_MAT_EXACT)) ? LTXW_DESC_EXACT : 0;
+        for (size_t l = l0; l < l1; ++l)
+          d.loras[l - l0] = {base + p.off_b[l], base + p.off_a[l], (int32_t)p.deltas[l]->rank, p.deltas[l]->coeff,
+                             p.fdt[l], 0};
+        ltxw::DescEx ex = first ? p.ex : ltxw::DescEx{};
+        // FP8 sources keep the reference's one NaN through every pass.
+        ex.canon_nan = chained && ltxw::format_bytes(p.fmt) == 1 ? 1 : 0;
+        descs.push_back(d);
+        exs.push_back(ex);
+      }
     }
     if (int r2 = ltxw::run_descs(ctx, descs.data(), (int)descs.size(), exs.data())) {
       rc = sfail(r2, "%s", ctx->err.c_str());
@@ -774,6 +816,16 @@ int run_pipeline(ltxw_ctx* ctx, std::vector<Plan>& plans, int out_dtype, uint32_
   return rc;
 }
 
+int check_flags(uint32_t flags) {
+  const uint32_t all = LTXW_MAT_SCALE_FIRST | LTXW_MAT_EXACT | LTXW_MAT_ROW_SCALES | LTXW_MAT_MFMA;
+  if (flags & ~all) return sfail(LTXW_ERR_INVALID_ARG, "unknown flags 0x%x", flags);
+  if ((flags & LTXW_MAT_SCALE_FIRST) && (flags & LTXW_MAT_ROW_SCALES))
+    return sfail(LTXW_ERR_INVALID_ARG, "LTXW_MAT_SCALE_FIRST and LTXW_MAT_ROW_SCALES together");
+  if ((flags & LTXW_MAT_EXACT) && (flags & LTXW_MAT_MFMA))
+    return sfail(LTXW_ERR_INVALID_ARG, "LTXW_MAT_EXACT and LTXW_MAT_MFMA together");
+  return LTXW_OK;
+}
+
 int materialize(ltxw_store* s, ltxw_ctx* ctx, const char* const* keys, int64_t n_keys, int32_t out_dtype,
                 uint32_t flags, void* const* outs) {
   if (!s || !ctx) return sfail(LTXW_ERR_INVALID_ARG, "null store or context");
@@ -781,7 +833,9 @@ int materialize(ltxw_store* s, ltxw_ctx* ctx, const char* const* keys, int64_t n
     return sfail(LTXW_ERR_INVALID_ARG, "invalid key or output array");
   if (out_dtype != LTXW_OUT_BF16 && out_dtype != LTXW_OUT_F32)
     return sfail(LTXW_ERR_INVALID_ARG, "invalid output dtype %d", out_dtype);
-  if (flags & ~(LTXW_MAT_SCALE_FIRST | LTXW_MAT_EXACT)) return sfail(LTXW_ERR_INVALID_ARG, "unknown flags 0x%x", flags);
+  if (int rc = check_flags(flags)) return rc;
+  // The extensions are materialize's defaults.
+  flags &= ~(LTXW_MAT_ROW_SCALES | LTXW_MAT_MFMA);
   // Resolve and check every key before any work is queued.
   std::vector<Plan> plans;
   plans.reserve((size_t)n_keys);
@@ -1233,6 +1287,9 @@ int ltxw_store_materialize(ltxw_store* s, ltxw_ctx* ctx, const char* const* keys
 
 int ltxw_store_read(ltxw_store* s, ltxw_ctx* ctx, const char* key, uint32_t flags, float* out, int64_t n) {
   if (!s || !ctx || !key) return sfail(LTXW_ERR_INVALID_ARG, "null store, context or key");
+  if (int rc = check_flags(flags)) return rc;
+  // The reference's rules unless the caller opts into an extension.
+  flags = (flags & LTXW_MAT_ROW_SCALES ? 0u : LTXW_MAT_SCALE_FIRST) | (flags & LTXW_MAT_MFMA ? 0u : LTXW_MAT_EXACT);
   auto it = s->entries.find(key);
   if (it == s->entries.end()) return sfail(LTXW_ERR_MISSING_KEY, "missing key: \"%s\"", key);
   const uint64_t numel = it->second.numel;

@@ -39,6 +39,9 @@ _py.PyCapsule_New.restype = ctypes.py_object
 _py.PyCapsule_New.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p]
 _py.PyCapsule_GetPointer.restype = ctypes.c_void_p
 _py.PyCapsule_GetPointer.argtypes = [ctypes.py_object, ctypes.c_char_p]
+# The capsule destructor receives the capsule as a raw pointer.
+_IsValid = ctypes.PYFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_char_p)(("PyCapsule_IsValid", _py))
+_GetPointerRaw = ctypes.PYFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p, ctypes.c_char_p)(("PyCapsule_GetPointer", _py))
 
 # Managed tensors handed out and not yet released by their consumer.
 _live = {}
@@ -47,6 +50,17 @@ _live = {}
 @_DELETER
 def _release(mt):
     _live.pop(ctypes.addressof(mt.contents), None)
+
+
+@ctypes.CFUNCTYPE(None, ctypes.c_void_p)
+def _capsule_destructor(cap):
+    """DLPack producer rule: a capsule dropped without being consumed (its
+    name is still "dltensor"; a consumer renames it "used_dltensor" and calls
+    the deleter itself) releases its managed tensor here."""
+    if _IsValid(cap, b"dltensor"):
+        addr = _GetPointerRaw(cap, b"dltensor")
+        if addr:
+            _release(ctypes.cast(addr, ctypes.POINTER(DLManagedTensor)))
 
 
 def capsule(ptr, shape, bf16, device, owner):
@@ -68,7 +82,7 @@ def capsule(ptr, shape, bf16, device, owner):
     mt.manager_ctx = None
     mt.deleter = _release
     _live[ctypes.addressof(mt)] = (mt, shp, strd, owner)
-    return _py.PyCapsule_New(ctypes.addressof(mt), b"dltensor", None)
+    return _py.PyCapsule_New(ctypes.addressof(mt), b"dltensor", ctypes.cast(_capsule_destructor, ctypes.c_void_p))
 
 
 def view(cap):

@@ -18,6 +18,8 @@ DTYPE_NAMES = ["BOOL", "U8", "I8", "F8_E5M2", "F8_E4M3", "I16", "U16", "F16", "B
                "F32", "F64", "I64", "U64", "F8_E8M0", "F4", "F6_E2M3", "F6_E3M2", "C64"]
 MAT_SCALE_FIRST = 1
 MAT_EXACT = 2
+MAT_ROW_SCALES = 4
+MAT_MFMA = 8
 _MAX_DIMS = 16
 
 
@@ -263,7 +265,9 @@ class WeightStore:
         return out
 
     def read(self, key, ctx, flags=0):
-        """`read` (src/store.rs:479-521) on the device: (shape, f32 array)."""
+        """`read` (src/store.rs:479-521) on the device: (shape, f32 array),
+        bit-identical to the reference's unless `flags` opts into an
+        extension (MAT_ROW_SCALES, MAT_MFMA)."""
         shape = self.shape(key)
         out = np.empty(int(np.prod(shape, dtype=np.int64)), dtype=np.float32)
         N.check_store(N.lib().ltxw_store_read(self.h, ctx.h, key.encode(), flags, out.ctypes.data, out.size))

@@ -23,6 +23,8 @@
  *   7 per-row scale indexed by column
  *   8 alpha default 1 instead of rank
  *   9 e5m2 exponent bias 16 instead of 15
+ *  10 f16 subnormal step 2^-25 instead of 2^-24
+ *  11 f16 NaN without the quiet bit
  */
 static int g_mutation = 0;
 void orc_set_mutation(int m) { g_mutation = m; }
@@ -79,10 +81,10 @@ float orc_f16_to_f32(uint16_t h) {
   uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
   if (e == 31) {
     if (m == 0) return f_from_bits(sign | 0x7F800000u);
-    return f_from_bits(sign | 0x7FC00000u | (m << 13));
+    return f_from_bits(sign | (g_mutation == 11 ? 0x7F800000u : 0x7FC00000u) | (m << 13));
   }
   if (e == 0) {
-    float mag = (float)m * 0x1p-24f;
+    float mag = (float)m * (g_mutation == 10 ? 0x1p-25f : 0x1p-24f);
     return f_from_bits(sign | bits_of(mag));
   }
   return f_from_bits(sign | ((e + 112u) << 23) | (m << 13));

@@ -12,3 +12,17 @@ for p in (TESTS, os.path.join(ROOT, "ltx-rust_amd"), ROOT):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+
+
+def pytest_sessionfinish(session, exitstatus):
+    """Write the per-call statistics of the LoRA tolerance check (max ulp
+    distance, elements beyond 1 ulp, Frobenius errors) of a GPU session to
+    gpurun_out/parity_stats.json, when that directory exists."""
+    gu = sys.modules.get("gpu_util")
+    out_dir = os.path.join(ROOT, "gpurun_out")
+    if gu is None or not getattr(gu, "STATS", None) or not os.path.isdir(out_dir):
+        return
+    import json
+
+    with open(os.path.join(out_dir, "parity_stats.json"), "w") as f:
+        json.dump(gu.STATS, f, indent=0)

@@ -73,6 +73,29 @@ def check_decode_extremes():
     return (not bad, "; ".join(bad))
 
 
+def check_f16_widening():
+    """F16 -> f32 widening (half 2.7.1 `f16::to_f32`, used by store.rs:690-705
+    for F16 bases and lora.rs:186-193 for F16 factors) against numpy's
+    independent binary16 conversion on all 65536 codes, read as little-endian
+    bytes through the oracle's dtype dispatch. Finite codes and infinities
+    must match bit for bit; NaN codes must be NaN with numpy's sign and
+    payload (mantissa << 13), plus the quiet bit that half's `to_f32` sets."""
+    codes = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    mine = O.decode(codes, O.F16).view(np.uint32)
+    theirs = codes.view(np.float16).astype(np.float32).view(np.uint32)
+    nan_c = ((codes & 0x7C00) == 0x7C00) & ((codes & 0x03FF) != 0)
+    conds = [
+        (np.array_equal(mine[~nan_c], theirs[~nan_c]), "finite codes and infinities differ from numpy"),
+        (np.all(np.isnan(mine[nan_c].view(np.float32))), "NaN codes must widen to NaN"),
+        (np.array_equal(mine[nan_c] | 0x00400000, theirs[nan_c] | 0x00400000), "NaN sign or payload differs"),
+        (np.all(mine[nan_c] & 0x00400000), "widened NaNs must be quiet"),
+        (mine[0x0001] == 0x33800000, "smallest subnormal 2^-24"),
+        (mine[0x7BFF] == np.float32(65504.0).view(np.uint32), "largest finite 65504"),
+    ]
+    bad = [m for ok, m in conds if not ok]
+    return (not bad, "; ".join(bad))
+
+
 def check_fp8_fixture():
     """crates/ltx-weights/tests/parity.rs:51-75 with its fixtures; bit-exact."""
     src = load_fixture_tensors("fp8_e4m3fn_parity")
@@ -205,6 +228,7 @@ def check_negative_zero_scaled():
 
 ALL_CHECKS = [
     check_fp8_unit_kats,
+    check_f16_widening,
     check_decode_extremes,
     check_fp8_fixture,
     check_lora_fixture,

@@ -1,5 +1,7 @@
 """Helpers for the GPU parity tests: run a case through the C ABI and compare
 it with the CPU oracle under the stated tolerances."""
+import os
+
 import numpy as np
 
 import ltx_weights as lw
@@ -102,20 +104,28 @@ def bf16_to_f64(u16):
     return (u16.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
 
 
-def compare_lora_bf16(case, got, row_sel=None):
+# Statistics of every compare_lora_bf16 call in this process, in call order
+# (the GPU test session writes them out; see conftest.py).
+STATS = []
+
+
+def compare_lora_bf16(case, got, row_sel=None, label=None):
     """Tolerance for the fused path (MFMA summation order differs from the
     reference's sequential FMA chain):
-      (1) every element within 1 bf16 ulp (ordered distance) of RNE(reference f32),
-          except
-      (2) elements where the f32 accumulation error of either order can move
-          the result across more than one bf16 step: there the output must be
-          within 0.5 ulp_bf16 + 2*(rank_total+4)*2^-24*(|deq| + sum|c B A|)
-          of the exact value, and such elements must be rare (< 1e-4);
+      (1) every element within 1 bf16 ulp (ordered distance) of the
+          reference's own result RNE(reference f32), except
+      (2) elements further away than that must be no farther from the exact
+          value W64 (f64 sum of the same terms) than the reference's f32 is:
+          |gpu - W64| <= |ref32 - W64|, i.e. only where the reference's own
+          chain has lost more than a bf16 step to rounding;
       (3) ||out - RNE(W64)||_F / ||W64||_F <= 1e-3 (Frobenius, against the
           bf16-rounded f64 oracle; bf16 rounding alone is ~1.7e-3 against the
           unrounded value, which is reported too).
-    Returns a dict of statistics; raises AssertionError on failure."""
-    ref = oracle_bf16(case, row_sel)
+    NaN positions and encodings must match exactly.
+    Returns a dict of statistics (also appended to STATS); raises
+    AssertionError on failure."""
+    ref32 = oracle_f32(case, row_sel)
+    ref = O.read_bf16(ref32, O.F32, threads=16)
     got = np.asarray(got)
     nan_r = np.isnan(bf16_to_f64(ref))
     nan_g = np.isnan(bf16_to_f64(got))
@@ -124,19 +134,23 @@ def compare_lora_bf16(case, got, row_sel=None):
     d = np.abs(bf16_ordered(got) - bf16_ordered(ref))
     d[nan_r] = 0
     bad = d > 1
-    stats = {"n": int(got.size), "max_ulp": int(d.max()) if d.size else 0, "n_over_1ulp": int(bad.sum())}
+    stats = {"n": int(got.size), "max_ulp": int(d.max()) if d.size else 0, "n_over_1ulp": int(bad.sum()),
+             "label": label or case.get("label") or os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0], "shape": [int(x) for x in got.shape]}
+    STATS.append(stats)
     w, f, m, s, loras = oracle_args(case, row_sel)
     w64 = O.read_f64_rows(w, f, m, s, loras)
     g64 = bf16_to_f64(got)
     if bad.any():
-        bound = O.abs_bound_rows(w, f, m, s, loras)
-        rank_total = sum(l[2] for l in case["loras"])
-        lim = 0.5 * np.abs(g64) * 2.0 ** -8 + 2 * (rank_total + 4) * 2.0 ** -24 * bound
-        err = np.abs(g64 - w64)
-        assert np.all(err[bad] <= lim[bad]), (
-            "%d elements beyond 1 ulp and beyond the f32 error bound (worst err/lim %.3g)"
-            % (int(np.sum(err[bad] > lim[bad])), float(np.max(err[bad] / lim[bad]))))
-        assert bad.mean() < 1e-4, "too many ill-conditioned elements: %d" % int(bad.sum())
+        err_gpu = np.abs(g64 - w64)
+        err_ref = np.abs(ref32.astype(np.float64) - w64)
+        worse = bad & ~(err_gpu <= err_ref)
+        stats["over_1ulp"] = [
+            {"flat": int(k), "gpu": int(got.flat[k]), "ref_bf16": int(ref.flat[k]),
+             "err_gpu": float(err_gpu.flat[k]), "err_ref32": float(err_ref.flat[k])}
+            for k in np.flatnonzero(bad)[:8]]
+        assert not worse.any(), (
+            "%d elements beyond 1 ulp of the reference and farther from the exact value than its f32 (%s)"
+            % (int(worse.sum()), stats["over_1ulp"]))
     fin = np.isfinite(w64) & np.isfinite(g64)
     r64 = bf16_to_f64(bf16_from_f64_exact(w64))
     den = np.linalg.norm(w64[fin])

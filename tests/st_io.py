@@ -56,3 +56,22 @@ def write(path, tensors, metadata=None):
         f.write(hb)
         for p in parts:
             f.write(p)
+
+
+def open_mmap(path):
+    """{name: (dtype, shape, read-only memory-mapped array of the storage
+    type)} of a safetensors file; reads only the header, so sampled rows of
+    a multi-GB file cost only their own pages."""
+    with open(path, "rb") as f:
+        (hlen,) = struct.unpack("<Q", f.read(8))
+        header = json.loads(f.read(hlen).decode("utf-8"))
+    header.pop("__metadata__", None)
+    base = 8 + hlen
+    out = {}
+    for name, info in header.items():
+        s, e = info["data_offsets"]
+        dt = STORAGE[info["dtype"]]
+        n = (e - s) // np.dtype(dt).itemsize
+        arr = np.memmap(path, dtype=dt, mode="r", offset=base + s, shape=(n,)) if n else np.zeros(0, dt)
+        out[name] = (info["dtype"], list(info["shape"]), arr)
+    return out

@@ -536,6 +536,44 @@ def test_upload_download_round_trip(ctx):
         ctx.free(p)
 
 
+def test_upload_is_ordered_after_queued_work(ctx):
+    """ltxw_upload runs in call order: refilling a device buffer while a
+    kernel that reads it is still queued, or right after a queued memset of
+    it, gives every operation the data it was queued with."""
+    log("case: upload ordering")
+    rng = np.random.default_rng(12)
+    rows, cols = 2048, 4096
+    cases = [synth.tensor_case(1200 + k, rows, cols, synth.E4M3FN, synth.SCALE_TENSOR, loras=()) for k in range(3)]
+    x = ctx.alloc(rows * cols)
+    sc = ctx.alloc(4 * 3)
+    outs = [ctx.alloc(rows * cols * 2) for _ in cases]
+    try:
+        for k, c in enumerate(cases):
+            ctx.upload(c["scales"], sc + 4 * k)
+        # Queue: several big kernels ahead, then dequant(x) -> out0, refill x,
+        # dequant(x) -> out1, memset x, refill x, dequant(x) -> out2.
+        busy = ctx.alloc(rows * cols * 2)
+        for _ in range(8):
+            ctx.dequant(x, rows, cols, lw.FMT_E4M3FN, lw.SCALE_TENSOR, sc, busy)
+        ctx.upload(cases[0]["w"], x)
+        ctx.dequant(x, rows, cols, lw.FMT_E4M3FN, lw.SCALE_TENSOR, sc, outs[0])
+        ctx.upload(cases[1]["w"], x)
+        ctx.dequant(x, rows, cols, lw.FMT_E4M3FN, lw.SCALE_TENSOR, sc + 4, outs[1])
+        ctx.memset(x, 0, rows * cols)
+        ctx.upload(cases[2]["w"], x)
+        ctx.dequant(x, rows, cols, lw.FMT_E4M3FN, lw.SCALE_TENSOR, sc + 8, outs[2])
+        ctx.synchronize()
+        ctx.free(busy)
+        for c, o in zip(cases, outs):
+            got = np.empty((rows, cols), np.uint16)
+            ctx.download(o, got)
+            assert np.array_equal(got, U.oracle_bf16(c))
+    finally:
+        for p in [x, sc] + outs:
+            ctx.free(p)
+    del rng
+
+
 # ---------------------------------------------------------------------------
 # Exact mode (LTXW_DESC_EXACT): the reference's own operation order, bit for bit
 # ---------------------------------------------------------------------------

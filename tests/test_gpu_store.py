@@ -17,7 +17,7 @@ import ltx_weights as lw
 import oracle_lib as O
 import st_io
 from ltx_weights import synth
-from ltx_weights.store import MAT_EXACT, MAT_SCALE_FIRST, KeyMap, LoraFile, WeightStore
+from ltx_weights.store import MAT_EXACT, MAT_MFMA, MAT_ROW_SCALES, MAT_SCALE_FIRST, KeyMap, LoraFile, WeightStore
 
 pytestmark = pytest.mark.gpu
 
@@ -106,6 +106,65 @@ def test_lora_merge_basic_alpha_and_stacking_values(ctx, tmp):
     assert store.read("s.weight", ctx)[1].tolist() == [[5, 6], [4, 8]]
 
 
+def _fixture_file(tmp, stem):
+    """A reference fixture (crates/ltx-weights/tests/fixtures/<stem>.safetensors)
+    rewritten from the committed vectors, with its metadata."""
+    import json
+
+    import golden_checks as G
+
+    with open(G.REF_FIXTURES) as f:
+        meta = json.load(f)["files"][stem]["metadata"]
+    ts = [(name, dt, shape, arr) for name, (dt, shape, arr) in G.load_fixture_tensors(stem).items()]
+    return tmp(ts, meta or None)
+
+
+def test_reference_parity_fixture_lora_merge_bf16(ctx, tmp):
+    """crates/ltx-weights/tests/parity.rs:23-47 through the device path: bf16
+    base, f32 rank-2 factors with alpha 4, strength 0.75. The reference
+    allows 5e-2; here `read` must equal the oracle's f32 bit for bit and its
+    bf16 rounding (read, and materialize in both orders) must equal the
+    fixture's expected bf16 tensor, 32/32."""
+    log("reference fixture: lora parity")
+    store = WeightStore.open([_fixture_file(tmp, "lora_parity_base")])
+    report = store.merge_lora(LoraFile.open(_fixture_file(tmp, "lora_parity_lora")), 0.75)
+    assert "layer.weight" in report.matched_keys
+    got = store.read("layer.weight", ctx)[1]
+    expected_store = WeightStore.open([_fixture_file(tmp, "lora_parity_expected")])
+    expected = expected_store.read("layer.weight", ctx)[1]
+    assert got.shape == expected.shape == (8, 4)
+    assert np.all(np.abs(got - expected) <= 5e-2)  # the reference's own bar
+    import golden_checks as G
+
+    base, a, b, alpha, exp_bits = G.lora_fixture_inputs()
+    want = O.read_f32(base, O.BF16, loras=[(b, a, O.F32, O.lora_coeff(0.75, alpha, 2))])
+    assert np.array_equal(bits(got), bits(want))
+    assert np.array_equal(O.read_bf16(got, O.F32), exp_bits)
+    for flags in (0, MAT_EXACT):
+        t = store.materialize_bf16(ctx, ["layer.weight"], flags=flags)["layer.weight"]
+        try:
+            assert np.array_equal(t.to_numpy(), exp_bits), flags
+        finally:
+            t.free()
+
+
+def test_reference_parity_fixture_fp8_e4m3fn_with_scale(ctx, tmp):
+    """crates/ltx-weights/tests/parity.rs:51-75 through the device path:
+    4x4 e4m3fn with a scalar scale; 16/16 f32 bit-identical to the fixture's
+    expected tensor (the reference allows 1e-5)."""
+    log("reference fixture: fp8 parity")
+    store = WeightStore.open([_fixture_file(tmp, "fp8_e4m3fn_parity")])
+    got = store.read("w", ctx)[1]
+    expected = WeightStore.open([_fixture_file(tmp, "fp8_e4m3fn_expected")]).read("w", ctx)[1]
+    assert got.shape == expected.shape == (4, 4)
+    assert np.array_equal(bits(got), bits(expected))
+    t = store.materialize_bf16(ctx, ["w"])["w"]
+    try:
+        assert np.array_equal(t.to_numpy(), O.read_bf16(expected, O.F32))
+    finally:
+        t.free()
+
+
 def test_read_errors(ctx, tmp):
     p = tmp([("w", "I32", [2], np.array([42, -1], np.int32)), ("x", "F32", [1], f32(0))])
     s = WeightStore.open([p])
@@ -177,7 +236,7 @@ def test_reference_order_paths_bit_exact(ctx, tmp, base_dt, factor_dt, ranks, sh
         loras.append((b.reshape(rows, r), a.reshape(r, cols), FACTOR_DT[factor_dt], O.lora_coeff(strength, None, r)))
     smode = {None: O.SCALE_NONE, "row": O.SCALE_ROW, "tensor": O.SCALE_TENSOR}[scale]
     want = O.read_f32(w.reshape(rows, cols), O.DTYPE_CODES[base_dt], smode, sc, loras)
-    got = store.read("t.weight", ctx, flags=MAT_EXACT)[1]
+    got = store.read("t.weight", ctx, flags=MAT_ROW_SCALES)[1]  # reference order is read's default
     assert np.array_equal(bits(got), bits(want))
     # bf16 materialisation of the same key = RNE of that f32.
     out = store.materialize_bf16(ctx, ["t.weight"], flags=MAT_EXACT)["t.weight"]
@@ -207,8 +266,10 @@ def test_fused_path_through_store(ctx, tmp):
 
 
 def test_scale_policy_and_dtypes(ctx, tmp):
-    """[rows] scales are per row by default and element 0 under the
-    reference's rule (LTXW_MAT_SCALE_FIRST); scales in bf16/f16 widen exactly."""
+    """`read` follows the reference's rule: every scale tensor scales by its
+    element 0 (store.rs:498-508, :732-735), also one of shape[0] elements;
+    MAT_ROW_SCALES (and materialize by default) scales row o by element o.
+    Scales in bf16/f16 widen exactly."""
     log("scale policy")
     rng = np.random.default_rng(4)
     rows, cols = 16, 64
@@ -216,10 +277,24 @@ def test_scale_policy_and_dtypes(ctx, tmp):
     s16 = synth.bf16_from_f64(rng.uniform(1e-3, 1e-1, rows))
     store = WeightStore.open([tmp([("w", "F8_E4M3", [rows, cols], w), ("w_scale", "BF16", [rows], s16)])])
     sc = O.decode(s16, O.BF16)
-    got_row = store.read("w", ctx)[1]
-    assert np.array_equal(bits(got_row), bits(O.read_f32(w, O.E4M3FN, O.SCALE_ROW, sc)))
-    got_first = store.read("w", ctx, flags=MAT_SCALE_FIRST)[1]
-    assert np.array_equal(bits(got_first), bits(O.read_f32(w, O.E4M3FN, O.SCALE_TENSOR, sc[:1])))
+    want_first = O.read_f32(w, O.E4M3FN, O.SCALE_TENSOR, sc[:1])
+    want_row = O.read_f32(w, O.E4M3FN, O.SCALE_ROW, sc)
+    assert np.array_equal(bits(store.read("w", ctx)[1]), bits(want_first))
+    assert np.array_equal(bits(store.read("w", ctx, flags=MAT_SCALE_FIRST)[1]), bits(want_first))
+    assert np.array_equal(bits(store.read("w", ctx, flags=MAT_ROW_SCALES)[1]), bits(want_row))
+    for flags, want in ((0, want_row), (MAT_SCALE_FIRST, want_first)):
+        out = ctx.alloc(rows * cols * 4)
+        try:
+            store.materialize(ctx, ["w"], [out], lw.OUT_F32, flags)
+            got = np.empty((rows, cols), np.float32)
+            ctx.download(out, got)
+            assert np.array_equal(bits(got), bits(want)), flags
+        finally:
+            ctx.free(out)
+    with pytest.raises(lw.InvalidArgument):
+        store.read("w", ctx, flags=MAT_SCALE_FIRST | MAT_ROW_SCALES)
+    with pytest.raises(lw.InvalidArgument):
+        store.read("w", ctx, flags=MAT_EXACT | MAT_MFMA)
     # A scale of another length scales by element 0 (store.rs:732-735).
     store2 = WeightStore.open([tmp([("w", "F8_E4M3", [rows, cols], w),
                                     ("w_scale", "F16", [3], np.array([0.5, 2, 4], np.float16).view(np.uint16))])])
@@ -228,6 +303,47 @@ def test_scale_policy_and_dtypes(ctx, tmp):
     neg0 = np.full((2, 8), 0x80, np.uint8)
     store3 = WeightStore.open([tmp([("z", "F8_E4M3", [2, 8], neg0), ("z_scale", "F32", [0], np.zeros(0, np.float32))])])
     assert np.all(bits(store3.read("z", ctx)[1]) == 0)
+
+
+def test_read_is_reference_read_with_row_sized_scale_and_six_loras(ctx, tmp):
+    """The frozen `read` on a key with a shape[0]-element scale sibling and six
+    stacked LoRAs (store.rs:498-515, :635-637, :732-735): bit-identical to the
+    oracle's element-0 scale and merge-order FMA chain. materialize runs the
+    same six deltas in the reference's order (passes of up to four through an
+    f32 accumulator): f32 bit-identical, bf16 its RNE."""
+    log("read: row-sized scale, six LoRAs")
+    rng = np.random.default_rng(66)
+    rows, cols = 96, 200
+    w = synth.E4M3FN_CODES[rng.integers(0, 254, (rows, cols))]
+    sc = rng.uniform(1e-3, 1e-1, rows).astype(np.float32)
+    store = WeightStore.open([tmp([("m.weight", "F8_E4M3", [rows, cols], w), ("m.weight_scale", "F32", [rows], sc)])])
+    ranks = [8, 16, 3, 32, 5, 64]
+    dts = ["BF16", "F32", "F16", "BF16", "F8_E4M3", "BF16"]
+    strengths = [1.0, 0.5, -0.75, 0.25, 2.0, 0.125]
+    loras = []
+    for r, dt, st in zip(ranks, dts, strengths):
+        a = factor_bits(rng, dt, (r, cols), 0.05)
+        b = factor_bits(rng, dt, (rows, r), 0.05)
+        store.merge_lora(LoraFile.open(tmp([("m.lora_A.weight", dt, [r, cols], a),
+                                            ("m.lora_B.weight", dt, [rows, r], b)])), st)
+        loras.append((b.reshape(rows, r), a.reshape(r, cols), FACTOR_DT[dt], O.lora_coeff(st, None, r)))
+    assert len(store.deltas("m.weight")) == 6
+    want = O.read_f32(w, O.E4M3FN, O.SCALE_TENSOR, sc[:1], loras)
+    assert np.array_equal(bits(store.read("m.weight", ctx)[1]), bits(want))
+    want_row = O.read_f32(w, O.E4M3FN, O.SCALE_ROW, sc, loras)
+    out = ctx.alloc(rows * cols * 4)
+    try:
+        store.materialize(ctx, ["m.weight"], [out], lw.OUT_F32)
+        got = np.empty((rows, cols), np.float32)
+        ctx.download(out, got)
+        assert np.array_equal(bits(got), bits(want_row))
+    finally:
+        ctx.free(out)
+    t = store.materialize_bf16(ctx, ["m.weight"])["m.weight"]
+    try:
+        assert np.array_equal(t.to_numpy(), O.read_bf16(w, O.E4M3FN, O.SCALE_ROW, sc, loras))
+    finally:
+        t.free()
 
 
 def test_multidim_empty_and_errors(ctx, tmp):
@@ -241,12 +357,11 @@ def test_multidim_empty_and_errors(ctx, tmp):
     assert got.shape == (4, 3, 5)
     assert np.array_equal(bits(got).ravel(), bits(O.decode(w3.ravel(), O.E4M3FN)))
     assert store.read("e", ctx)[1].shape == (0, 7)
-    # Five stacked LoRAs exceed the device path's limit of four.
+    # Five stacked LoRAs (more than one launch takes) all apply, in merge order.
     for k in range(5):
         store.merge_lora(LoraFile.open(tmp([("m.lora_A.weight", "F32", [1, 3], f32(1, 1, 1)),
-                                            ("m.lora_B.weight", "F32", [2, 1], f32(1, 1))])), 1.0)
-    with pytest.raises(lw.UnsupportedDtype):
-        store.read("m.weight", ctx)
+                                            ("m.lora_B.weight", "F32", [2, 1], f32(1, k))])), 1.0)
+    assert store.read("m.weight", ctx)[1].tolist() == [[5, 5, 5], [10, 10, 10]]
     with pytest.raises(lw.InvalidArgument):
         store.materialize(ctx, ["c"], [None])
     with pytest.raises(lw.MissingKey):

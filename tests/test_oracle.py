@@ -62,6 +62,18 @@ def test_bf16_rne_matches_torch():
     assert np.array_equal(mine[~finite], ((nanx >> 16) | 0x40).astype(np.uint16))
 
 
+def test_f16_widening_matches_torch_all_codes():
+    """A second independent binary16 implementation (torch) on every
+    non-NaN code; NaN codes as a class."""
+    torch = pytest.importorskip("torch")
+    codes = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    mine = O.decode(codes, O.F16)
+    theirs = torch.from_numpy(codes.view(np.int16).copy()).view(torch.float16).float().numpy()
+    nan_m, nan_t = np.isnan(mine), np.isnan(theirs)
+    assert np.array_equal(nan_m, nan_t)
+    assert np.array_equal(mine[~nan_m].view(np.uint32), theirs[~nan_t].view(np.uint32))
+
+
 def test_f32_mt_is_bit_identical_to_single_thread():
     w, scales, loras = G.random_case(67, 96, 8, seed=11, nloras=2)
     one = O.read_f32(w, O.E4M3FN, O.SCALE_ROW, scales, loras, threads=1)
@@ -70,7 +82,7 @@ def test_f32_mt_is_bit_identical_to_single_thread():
 
 
 # Every planted mistake must make at least one check fail.
-@pytest.mark.parametrize("mut", range(1, 10))
+@pytest.mark.parametrize("mut", range(1, 12))
 def test_checks_catch_planted_mistake(mut):
     failed = []
     with O.mutation(mut):
