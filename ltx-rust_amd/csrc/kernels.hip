@@ -450,38 +450,48 @@ __device__ __forceinline__ void dqt_store(const DequantTileArgs& a, uint32_t i0,
   }
 }
 
-template <int FMT, int SMODE, bool F32OUT, bool FULL>
-__device__ __forceinline__ void dqt_pair(const DequantTileArgs& a, uint32_t i0, uint32_t gA, uint32_t gB, bool hasB,
-                                         int tid, float tscale) {
-  u32x2 wa[8], wb[8];
-  float sa[8], sb[8];
-  dqt_load<SMODE, FULL>(a, i0, gA, tid, wa, sa, tscale);
-  if (hasB) dqt_load<SMODE, FULL>(a, i0, gB, tid, wb, sb, tscale);
-  dqt_store<FMT, SMODE, F32OUT, FULL>(a, i0, gA, tid, wa, sa);
-  if (hasB) dqt_store<FMT, SMODE, F32OUT, FULL>(a, i0, gB, tid, wb, sb);
+// U units of a band: every unit's bytes are requested before the first unit
+// is converted.
+template <int FMT, int SMODE, bool F32OUT, bool FULL, int U>
+__device__ __forceinline__ void dqt_units(const DequantTileArgs& a, uint32_t i0, uint32_t g0, int tid, float tscale) {
+  u32x2 w[U][8];
+  float sc[U][8];
+#pragma unroll
+  for (int u = 0; u < U; ++u) dqt_load<SMODE, FULL>(a, i0, g0 + kUnitRows * u, tid, w[u], sc[u], tscale);
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (FULL || g0 + kUnitRows * u < a.rows) dqt_store<FMT, SMODE, F32OUT, FULL>(a, i0, g0 + kUnitRows * u, tid, w[u], sc[u]);
 }
 
-template <int FMT, int SMODE, bool F32OUT>
+template <int FMT, int SMODE, bool F32OUT, int U>
 __global__ __launch_bounds__(256) void k_dequant_tile(DequantTileArgs a) {
   const int tid = threadIdx.x;
   const uint32_t p = blockIdx.x;
   const uint32_t i0 = (p % a.bands_n) * kBandCols;
-  const uint32_t gA = (p / a.bands_n) * kPairRows;
-  const uint32_t gB = gA + kWavesPerGroup * kStripRows;
-  const bool hasB = gB < a.rows;
-  const bool full = gA + kPairRows <= a.rows && i0 + kBandCols <= a.cols;
+  const uint32_t g0 = (p / a.bands_n) * (U * kUnitRows);
+  const bool full = g0 + U * kUnitRows <= a.rows && i0 + kBandCols <= a.cols;
   const float tscale = SMODE == 1 ? *G(uni_ptr(a.scales)) : 1.0f;
-  if (full) dqt_pair<FMT, SMODE, F32OUT, true>(a, i0, gA, gB, hasB, tid, tscale);
-  else dqt_pair<FMT, SMODE, F32OUT, false>(a, i0, gA, gB, hasB, tid, tscale);
+  if (full) dqt_units<FMT, SMODE, F32OUT, true, U>(a, i0, g0, tid, tscale);
+  else dqt_units<FMT, SMODE, F32OUT, false, U>(a, i0, g0, tid, tscale);
+}
+
+template <int FMT, int SMODE, int U>
+hipError_t dequant_tile_u(const DequantTileArgs& a, bool f32out, dim3 grid, hipStream_t s) {
+  if (f32out)
+    hipLaunchKernelGGL((k_dequant_tile<FMT, SMODE, true, U>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((k_dequant_tile<FMT, SMODE, false, U>), grid, dim3(256), 0, s, a);
+  return hipGetLastError();
 }
 
 template <int FMT, int SMODE>
 hipError_t dequant_tile_out(const DequantTileArgs& a, bool f32out, dim3 grid, hipStream_t s) {
-  if (f32out)
-    hipLaunchKernelGGL((k_dequant_tile<FMT, SMODE, true>), grid, dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL((k_dequant_tile<FMT, SMODE, false>), grid, dim3(256), 0, s, a);
-  return hipGetLastError();
+  switch (a.units) {
+    case 1: return dequant_tile_u<FMT, SMODE, 1>(a, f32out, grid, s);
+    case 2: return dequant_tile_u<FMT, SMODE, 2>(a, f32out, grid, s);
+    case 4: return dequant_tile_u<FMT, SMODE, 4>(a, f32out, grid, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <int FMT>
@@ -524,9 +534,11 @@ hipError_t launch_dequant(const DequantArgs& a, int fmt, int scale_mode, bool f3
 
 hipError_t launch_dequant_tile(const DequantTileArgs& a, int fmt, int scale_mode, bool f32out,
                                hipStream_t stream) {
-  const uint64_t pairs = (uint64_t)a.bands_n * ((a.rows + kPairRows - 1) / kPairRows);
-  if (pairs == 0) return hipSuccess;
-  dim3 grid((unsigned)pairs);
+  if (a.units != 1 && a.units != 2 && a.units != 4) return hipErrorInvalidValue;
+  const uint64_t rows_per = (uint64_t)a.units * kUnitRows;
+  const uint64_t groups = (uint64_t)a.bands_n * ((a.rows + rows_per - 1) / rows_per);
+  if (groups == 0) return hipSuccess;
+  dim3 grid((unsigned)groups);
   return fmt == 0 ? dequant_tile_scale<0>(a, scale_mode, f32out, grid, stream)
                   : dequant_tile_scale<1>(a, scale_mode, f32out, grid, stream);
 }

@@ -575,7 +575,7 @@ def test_mixed_factor_types_on_one_tensor(ctx, tmp):
                                         ("x.lora_B.weight", "F32", [rows, 8], b2)])), 0.5)
     want = O.read_f32(w, O.E4M3FN, O.SCALE_ROW, sc, [(b1, a1, O.BF16, O.lora_coeff(1.0, None, 16)),
                                                      (b2, a2, O.F32, O.lora_coeff(0.5, None, 8))])
-    assert np.array_equal(bits(store.read("x.weight", ctx)[1]), bits(want))
+    assert np.array_equal(bits(store.read("x.weight", ctx, flags=MAT_ROW_SCALES)[1]), bits(want))
 
 
 def test_materialise_small_staging_slots_many_tensors(tmp):
