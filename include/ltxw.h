@@ -171,6 +171,21 @@ int ltxw_dequant_lora(ltxw_ctx* ctx, const uint8_t* w, int64_t rows, int64_t col
  * `Scope::tensor` -> `read` over a block's linears (ltx-dit src/load.rs:149-170). */
 int ltxw_dequant_lora_grouped(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n);
 
+/* ltxw_dequant_lora_grouped for callers that cannot allocate memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid it): the
+ * same kernels and results (bit-identical), but no allocation of any kind
+ * on the device or in pinned host memory. The job tables of its launches go
+ * to a static device array of 64 KiB per device (held until the process
+ * ends), filled by small kernel launches that carry the table in their
+ * arguments; calls with more than LTXW_NOALLOC_MAX_DESCS descriptors are
+ * rejected (LTXW_ERR_INVALID_ARG) before anything is queued. Every context
+ * on a device shares its array: calls queued on one context run in order,
+ * but calls from two contexts on the same device that overlap in time race.
+ * No counterpart in the reference (which has no device); added for callers
+ * that cannot allocate. */
+#define LTXW_NOALLOC_MAX_DESCS 128
+int ltxw_dequant_lora_grouped_noalloc(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n);
+
 /* The context's compute stream (a hipStream_t), for callers that time or
  * order their own work against ltxw's. */
 void* ltxw_ctx_stream(ltxw_ctx* ctx);

@@ -318,6 +318,16 @@ int take_table(ltxw_ctx* ctx, size_t bytes, ltxw_ctx::TableSlot** out, bool* rec
   return LTXW_OK;
 }
 
+// Device bytes of the job table of an allocation-free launch of n jobs: the
+// jobs, then (256-byte aligned) their first work units, rounded up to the
+// fill kernel's 16-byte words.
+constexpr size_t noalloc_table_bytes(size_t n) {
+  return ((((n * sizeof(ltxw::JobDev) + 255) & ~size_t(255)) + n * sizeof(int64_t)) + 15) & ~size_t(15);
+}
+static_assert(noalloc_table_bytes(LTXW_NOALLOC_MAX_DESCS) <= ltxw::kScratchBytes,
+              "the largest allocation-free call's job table fits the scratch array");
+static_assert(sizeof(ltxw::JobDev) % 16 == 0, "jobs fill whole 16-byte words");
+
 // Total padded LoRA rank of a job (its K extent in the LDS stage).
 int job_k(const ltxw::JobDev& j) {
   int k = 0;
@@ -328,7 +338,8 @@ int job_k(const ltxw::JobDev& j) {
 // One fused launch over `jobs` (all fused_ok, same out dtype, kernel, factor
 // type and K-steps): one workgroup per 128-column band and 256 rows of every
 // job.
-int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool multi, int fdt, bool base16) {
+int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool multi, int fdt, bool base16,
+              bool noalloc) {
   if (jobs.empty()) return LTXW_OK;
   int kmax = 0;
   for (auto& j : jobs) kmax = std::max(kmax, job_k(j));
@@ -346,6 +357,24 @@ int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool 
   t.lds_ld = kmax + 8;
   if (jobs.size() == 1) {
     t.one = jobs[0];
+  } else if (noalloc) {
+    // The table goes to the device scratch array, written by fill launches
+    // queued just before this launch: launches on this stream run in order,
+    // so the previous reader of the scratch has finished by then.
+    const size_t bytes = noalloc_table_bytes(jobs.size());
+    if (bytes > ltxw::kScratchBytes || !ctx->scratch)
+      return fail(ctx, LTXW_ERR_INVALID_ARG, "job table of %zu bytes exceeds the %zu-byte scratch", bytes,
+                  ltxw::kScratchBytes);
+    const size_t off_b = (jobs.size() * sizeof(ltxw::JobDev) + 255) & ~size_t(255);
+    alignas(16) int64_t begins[LTXW_NOALLOC_MAX_DESCS + 1] = {};
+    for (size_t k = 0; k < jobs.size(); ++k) begins[k] = jobs[k].unit_begin;
+    HIP_TRY(ctx, ltxw::launch_fill_words(ctx->scratch, jobs.data(), jobs.size() * sizeof(ltxw::JobDev), ctx->compute),
+            "job table fill");
+    HIP_TRY(ctx, ltxw::launch_fill_words((char*)ctx->scratch + off_b, begins, (jobs.size() * 8 + 15) & ~size_t(15),
+                                         ctx->compute),
+            "job table fill");
+    t.jobs = reinterpret_cast<const ltxw::JobDev*>(ctx->scratch);
+    t.begins = reinterpret_cast<const int64_t*>((char*)ctx->scratch + off_b);
   } else {
     size_t jb = jobs.size() * sizeof(ltxw::JobDev);
     size_t bb = jobs.size() * sizeof(int64_t);
@@ -374,7 +403,7 @@ int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool 
 
 }  // namespace
 
-int ltxw::run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n, const DescEx* ex) {
+int ltxw::run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n, const DescEx* ex, bool noalloc) {
   // Job tables are allocated on the calling thread's current device.
   HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
   // Validate everything before queuing anything.
@@ -410,7 +439,7 @@ int ltxw::run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n, const D
   }
   for (auto& kv : buckets) {
     int rc = run_fused(ctx, kv.second, std::get<0>(kv.first) == 1, std::get<1>(kv.first) == 1, std::get<3>(kv.first),
-                       std::get<4>(kv.first) == 1);
+                       std::get<4>(kv.first) == 1, noalloc);
     if (rc) return rc;
   }
   return LTXW_OK;
@@ -478,6 +507,7 @@ int ltxw_ctx_create(int device, size_t staging_bytes, int n_staging, ltxw_ctx** 
     return bail(LTXW_ERR_HIP, "copy stream", e);
   if ((e = hipEventCreateWithFlags(&c->compute_mark, hipEventDisableTiming)) != hipSuccess)
     return bail(LTXW_ERR_HIP, "event", e);
+  if ((e = ltxw::scratch_address(&c->scratch)) != hipSuccess) return bail(LTXW_ERR_HIP, "scratch address", e);
   c->tables.resize(2 * kTableGroup);
   for (auto& t : c->tables)
     if ((e = hipEventCreateWithFlags(&t.copied, hipEventDisableTiming)) != hipSuccess)
@@ -632,6 +662,15 @@ int ltxw_dequant_lora_grouped(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int 
   if (!ctx) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context");
   if (n < 0 || (n > 0 && !descs)) return fail(ctx, LTXW_ERR_INVALID_ARG, "invalid descriptor array");
   return ltxw::run_descs(ctx, descs, n);
+}
+
+int ltxw_dequant_lora_grouped_noalloc(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n) {
+  if (!ctx) return fail(ctx, LTXW_ERR_INVALID_ARG, "null context");
+  if (n < 0 || (n > 0 && !descs)) return fail(ctx, LTXW_ERR_INVALID_ARG, "invalid descriptor array");
+  if (n > LTXW_NOALLOC_MAX_DESCS)
+    return fail(ctx, LTXW_ERR_INVALID_ARG, "%d descriptors exceed the allocation-free call's limit of %d", n,
+                LTXW_NOALLOC_MAX_DESCS);
+  return ltxw::run_descs(ctx, descs, n, nullptr, true);
 }
 
 }  // extern "C"

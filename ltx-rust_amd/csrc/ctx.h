@@ -49,6 +49,10 @@ struct ltxw_ctx {
   // more LoRAs than one launch takes (grown on demand).
   void* tmp = nullptr;
   size_t tmp_bytes = 0;
+  // This device's copy of the allocation-free call's scratch array
+  // (hipGetSymbolAddress at context creation; shared by every context on
+  // the device).
+  void* scratch = nullptr;
   std::string err;
 };
 
@@ -75,8 +79,12 @@ struct DescEx {
 
 // Validates and queues the descriptors on the compute stream (the body of
 // ltxw_dequant_lora_grouped). `ex` (optional, n entries) routes descriptors
-// with extras to the reference-order kernel.
-int run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n, const DescEx* ex = nullptr);
+// with extras to the reference-order kernel. `noalloc`: job tables go to the
+// device scratch array through fill launches instead of the pinned / device
+// table ring (the body of ltxw_dequant_lora_grouped_noalloc; n <=
+// LTXW_NOALLOC_MAX_DESCS, checked by the caller).
+int run_descs(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int n, const DescEx* ex = nullptr,
+              bool noalloc = false);
 
 // Bytes per element of a base format (ltxw_format); 0 for an unknown one.
 inline int format_bytes(int fmt) {

@@ -176,4 +176,20 @@ __host__ __device__ inline int pad_rank(int rank) { return (rank + 31) / 32 * 32
 // One thread per element, reference operation order. Any shape, alignment.
 hipError_t launch_generic(const GenericArgs& a, bool f32out, hipStream_t stream);
 
+// Device scratch of the allocation-free grouped call
+// (ltxw_dequant_lora_grouped_noalloc): the job tables of its launches, in a
+// file-scope device array of kScratchBytes per device, held until the
+// process ends. Launches queued one after another on one stream reuse it
+// from offset 0 (each table is written just before the launch that reads
+// it); work from two streams on one device would race.
+constexpr size_t kScratchBytes = 64 * 1024;
+// Address of the calling thread's current device's copy of the scratch
+// array (hipGetSymbolAddress).
+hipError_t scratch_address(void** ptr);
+// Writes `bytes` (a multiple of 16) of host data to device memory at `dst`
+// (16-byte aligned) with kernel launches that carry the bytes as kernel
+// arguments: no copy engine, no staging buffer, stream-ordered like any
+// other launch.
+hipError_t launch_fill_words(void* dst, const void* src, size_t bytes, hipStream_t stream);
+
 }  // namespace ltxw

@@ -8,6 +8,8 @@
 // The hardware FP8 converts equal the closed form of fp8.rs:90-158 on every
 // finite and infinite code; for NaN codes they return 0xFFC00000 where the
 // reference returns f32::NAN (0x7FC00000), so NaN results are canonicalised.
+#include <cstring>
+
 #include "kernels_dev.h"
 
 namespace ltxw {
@@ -616,6 +618,48 @@ hipError_t launch_exact(const ExactArgs& a, bool f32out, hipStream_t stream) {
   }
 #undef LTXW_EXACT_LAUNCH
   return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free grouped call and the kernel that fills it.
+
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+hipError_t scratch_address(void** ptr) { return hipGetSymbolAddress(ptr, HIP_SYMBOL(scratch)); }
+
+namespace {
+
+constexpr int kFillWords = 224;  // 16-byte words per launch: 3.5 KiB of kernel arguments
+
+struct FillArgs {
+  u32x4* dst;
+  uint32_t n;  // words of this launch, <= kFillWords
+  uint32_t pad[1];
+  u32x4 words[kFillWords];
+};
+static_assert(sizeof(FillArgs) <= 4096, "kernel arguments of one fill launch");
+
+__global__ __launch_bounds__(256) void k_fill_words(FillArgs a) {
+  const uint32_t t = threadIdx.x;
+  if (t < a.n) a.dst[t] = a.words[t];
+}
+
+}  // namespace
+
+hipError_t launch_fill_words(void* dst, const void* src, size_t bytes, hipStream_t stream) {
+  if (bytes % 16 != 0 || reinterpret_cast<uintptr_t>(dst) % 16 != 0) return hipErrorInvalidValue;
+  const size_t words = bytes / 16;
+  for (size_t w0 = 0; w0 < words; w0 += kFillWords) {
+    FillArgs a;
+    a.dst = reinterpret_cast<u32x4*>(dst) + w0;
+    a.n = (uint32_t)std::min<size_t>(kFillWords, words - w0);
+    a.pad[0] = 0;
+    std::memcpy(static_cast<void*>(a.words), reinterpret_cast<const char*>(src) + 16 * w0, 16 * (size_t)a.n);
+    hipLaunchKernelGGL(k_fill_words, dim3(1), dim3(256), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_generic(const GenericArgs& a, bool f32out, hipStream_t stream) {

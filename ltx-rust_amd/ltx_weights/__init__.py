@@ -17,6 +17,7 @@ from ._native import (  # noqa: F401
     FMT_F16,
     FMT_F32,
     MAX_LORAS,
+    NOALLOC_MAX_DESCS,
     OUT_BF16,
     OUT_F32,
     SCALE_NONE,

@@ -18,6 +18,7 @@ FMT_E4M3FN, FMT_E5M2, FMT_BF16, FMT_F16, FMT_F32 = 0, 1, 2, 3, 4
 SCALE_NONE, SCALE_TENSOR, SCALE_ROW = 0, 1, 2
 OUT_BF16, OUT_F32 = 0, 1
 MAX_LORAS = 4
+NOALLOC_MAX_DESCS = 128  # LTXW_NOALLOC_MAX_DESCS
 
 
 class WeightError(Exception):
@@ -127,7 +128,8 @@ class KeyRule(ctypes.Structure):
 EXPORTS = [
     "ltxw_ctx_create", "ltxw_ctx_destroy", "ltxw_last_error", "ltxw_alloc", "ltxw_free",
     "ltxw_memset", "ltxw_upload", "ltxw_download", "ltxw_synchronize", "ltxw_dequant",
-    "ltxw_dequant_lora", "ltxw_dequant_lora_grouped", "ltxw_ctx_stream", "ltxw_ctx_set_host_threads",
+    "ltxw_dequant_lora", "ltxw_dequant_lora_grouped", "ltxw_dequant_lora_grouped_noalloc", "ltxw_ctx_stream",
+    "ltxw_ctx_set_host_threads",
     # include/ltxw_store.h
     "ltxw_store_last_error", "ltxw_store_open", "ltxw_store_close", "ltxw_store_n_keys",
     "ltxw_store_key", "ltxw_store_contains", "ltxw_store_tensor_info", "ltxw_store_metadata",
@@ -164,6 +166,7 @@ def lib():
     L.ltxw_dequant.argtypes = [vp, vp, i64, i64, i32, i32, vp, vp, i32]
     L.ltxw_dequant_lora.argtypes = [vp, vp, i64, i64, i32, i32, vp, ctypes.POINTER(Lora), i32, vp, i32]
     L.ltxw_dequant_lora_grouped.argtypes = [vp, ctypes.POINTER(TensorDesc), i32]
+    L.ltxw_dequant_lora_grouped_noalloc.argtypes = [vp, ctypes.POINTER(TensorDesc), i32]
     L.ltxw_ctx_stream.argtypes = [vp]
     L.ltxw_ctx_stream.restype = vp
     L.ltxw_ctx_set_host_threads.argtypes = [vp, i32]
@@ -303,6 +306,17 @@ class Context:
                 return
             descs = self.make_descs(descs)
         self._chk(lib().ltxw_dequant_lora_grouped(self.h, descs, len(descs)))
+
+    def grouped_noalloc(self, descs):
+        """As grouped, through ltxw_dequant_lora_grouped_noalloc: no device or
+        pinned allocation (job tables in the library's static device scratch),
+        at most NOALLOC_MAX_DESCS descriptors."""
+        if not isinstance(descs, ctypes.Array):
+            if not descs:
+                self._chk(lib().ltxw_dequant_lora_grouped_noalloc(self.h, None, 0))
+                return
+            descs = self.make_descs(descs)
+        self._chk(lib().ltxw_dequant_lora_grouped_noalloc(self.h, descs, len(descs)))
 
     @staticmethod
     def make_descs(descs):
