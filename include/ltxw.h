@@ -174,10 +174,11 @@ int ltxw_dequant_lora_grouped(ltxw_ctx* ctx, const ltxw_tensor_desc* descs, int 
 /* ltxw_dequant_lora_grouped for callers that cannot allocate memory (code
  * under HIP graph capture, serving loops, harnesses that forbid it): the
  * same kernels and results (bit-identical), but no allocation of any kind
- * on the device or in pinned host memory. The job tables of its launches go
- * to a static device array of 64 KiB per device (held until the process
- * ends), filled by small kernel launches that carry the table in their
- * arguments; calls with more than LTXW_NOALLOC_MAX_DESCS descriptors are
+ * on the device or in pinned host memory. Job tables too large for a
+ * launch's kernel arguments (more than about 20 tensors in one fused
+ * launch) go to a static device array of 64 KiB per device (held until the
+ * process ends), filled by small kernel launches that carry the table in
+ * their arguments; calls with more than LTXW_NOALLOC_MAX_DESCS descriptors are
  * rejected (LTXW_ERR_INVALID_ARG) before anything is queued. Every context
  * on a device shares its array: calls queued on one context run in order,
  * but calls from two contexts on the same device that overlap in time race.

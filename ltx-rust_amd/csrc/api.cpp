@@ -318,15 +318,33 @@ int take_table(ltxw_ctx* ctx, size_t bytes, ltxw_ctx::TableSlot** out, bool* rec
   return LTXW_OK;
 }
 
-// Device bytes of the job table of an allocation-free launch of n jobs: the
-// jobs, then (256-byte aligned) their first work units, rounded up to the
-// fill kernel's 16-byte words.
-constexpr size_t noalloc_table_bytes(size_t n) {
-  return ((((n * sizeof(ltxw::JobDev) + 255) & ~size_t(255)) + n * sizeof(int64_t)) + 15) & ~size_t(15);
-}
-static_assert(noalloc_table_bytes(LTXW_NOALLOC_MAX_DESCS) <= ltxw::kScratchBytes,
+// Bytes of one fused launch's job record with ks K-steps.
+constexpr size_t record_bytes(int ks) { return sizeof(ltxw::FusedJob) + (size_t)ks * sizeof(ltxw::StepDev); }
+static_assert(LTXW_NOALLOC_MAX_DESCS * record_bytes(ltxw::kMaxSteps) <= ltxw::kScratchBytes,
               "the largest allocation-free call's job table fits the scratch array");
-static_assert(sizeof(ltxw::JobDev) % 16 == 0, "jobs fill whole 16-byte words");
+
+// Writes the records of jobs [first, first + count) (plan_fused done) to dst.
+void write_records(const std::vector<ltxw::JobDev>& jobs, size_t first, size_t count, int ks, unsigned char* dst) {
+  for (size_t k = 0; k < count; ++k) {
+    const ltxw::JobDev& j = jobs[first + k];
+    ltxw::FusedJob h{};
+    h.w = j.w;
+    h.out = j.out;
+    h.scales = j.scales;
+    h.rows = (uint32_t)j.rows;
+    h.cols = (uint32_t)j.cols;
+    h.bands_n = (uint32_t)j.bands_n;
+    h.unit_begin = (uint32_t)j.unit_begin;
+    h.fmt = (uint32_t)j.fmt;
+    h.scale_mode = (uint32_t)j.scale_mode;
+    h.qmask = j.qmask;
+    h.cmul = j.cmul;
+    h.coeff_out = j.coeff_out;
+    unsigned char* r = dst + k * record_bytes(ks);
+    memcpy(r, &h, sizeof(h));
+    memcpy(r + sizeof(h), j.step, (size_t)ks * sizeof(ltxw::StepDev));
+  }
+}
 
 // Total padded LoRA rank of a job (its K extent in the LDS stage).
 int job_k(const ltxw::JobDev& j) {
@@ -351,42 +369,47 @@ int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool 
     units += (int64_t)j.bands_n * ((j.rows + group_rows - 1) / group_rows);
   }
   if (units > INT32_MAX) return fail(ctx, LTXW_ERR_INVALID_ARG, "launch of %lld work units is too large", (long long)units);
+  // Every job of the launch has the same K-steps (the launches are bucketed by them).
+  const int ks = kmax / 32;
+  const size_t rec = record_bytes(ks);
+  const size_t bytes = jobs.size() * rec;
   ltxw::JobTable t{};
   t.n_jobs = (int32_t)jobs.size();
   t.total_units = units;
   t.lds_ld = kmax + 8;
-  if (jobs.size() == 1) {
-    t.one = jobs[0];
+  t.rec_bytes = (int32_t)rec;
+  for (int k = 0; k < ltxw::kInlineBegins; ++k)
+    t.begins[k] = (size_t)k < jobs.size() ? (uint32_t)jobs[(size_t)k].unit_begin : UINT32_MAX;
+  // The single-LoRA kernel reads a one-job launch's JobDev from its fixed
+  // place in the arguments; the several-LoRA kernel reads the record.
+  if (jobs.size() == 1) t.one = jobs[0];
+  if (bytes <= (size_t)ltxw::kInlineTableBytes) {
+    // In the kernel arguments: no upload (a DiT block's 10 tensors fit).
+    write_records(jobs, 0, jobs.size(), ks, t.inl);
+    t.table = nullptr;
   } else if (noalloc) {
-    // The table goes to the device scratch array, written by fill launches
-    // queued just before this launch: launches on this stream run in order,
-    // so the previous reader of the scratch has finished by then.
-    const size_t bytes = noalloc_table_bytes(jobs.size());
+    // The device scratch array, written by fill launches queued just before
+    // this launch: launches on this stream run in order, so the previous
+    // reader of the scratch has finished by then.
     if (bytes > ltxw::kScratchBytes || !ctx->scratch)
       return fail(ctx, LTXW_ERR_INVALID_ARG, "job table of %zu bytes exceeds the %zu-byte scratch", bytes,
                   ltxw::kScratchBytes);
-    const size_t off_b = (jobs.size() * sizeof(ltxw::JobDev) + 255) & ~size_t(255);
-    alignas(16) int64_t begins[LTXW_NOALLOC_MAX_DESCS + 1] = {};
-    for (size_t k = 0; k < jobs.size(); ++k) begins[k] = jobs[k].unit_begin;
-    HIP_TRY(ctx, ltxw::launch_fill_words(ctx->scratch, jobs.data(), jobs.size() * sizeof(ltxw::JobDev), ctx->compute),
-            "job table fill");
-    HIP_TRY(ctx, ltxw::launch_fill_words((char*)ctx->scratch + off_b, begins, (jobs.size() * 8 + 15) & ~size_t(15),
-                                         ctx->compute),
-            "job table fill");
-    t.jobs = reinterpret_cast<const ltxw::JobDev*>(ctx->scratch);
-    t.begins = reinterpret_cast<const int64_t*>((char*)ctx->scratch + off_b);
+    alignas(16) unsigned char buf[ltxw::kInlineTableBytes];
+    const size_t per = (size_t)ltxw::kInlineTableBytes / rec;
+    for (size_t k = 0; k < jobs.size(); k += per) {
+      const size_t cnt = std::min(per, jobs.size() - k);
+      write_records(jobs, k, cnt, ks, buf);
+      HIP_TRY(ctx, ltxw::launch_fill_words((char*)ctx->scratch + k * rec, buf, cnt * rec, ctx->compute),
+              "job table fill");
+    }
+    t.table = ctx->scratch;
   } else {
-    size_t jb = jobs.size() * sizeof(ltxw::JobDev);
-    size_t bb = jobs.size() * sizeof(int64_t);
-    size_t off_b = (jb + 255) & ~size_t(255);
     ltxw_ctx::TableSlot* slot = nullptr;
     bool record = false;
-    int rc = take_table(ctx, off_b + bb, &slot, &record);
+    int rc = take_table(ctx, bytes, &slot, &record);
     if (rc) return rc;
-    memcpy(slot->host, jobs.data(), jb);
-    int64_t* begins = reinterpret_cast<int64_t*>((char*)slot->host + off_b);
-    for (size_t k = 0; k < jobs.size(); ++k) begins[k] = jobs[k].unit_begin;
-    hipError_t e = hipMemcpyAsync(slot->dev, slot->host, off_b + bb, hipMemcpyHostToDevice, ctx->compute);
+    write_records(jobs, 0, jobs.size(), ks, (unsigned char*)slot->host);
+    hipError_t e = hipMemcpyAsync(slot->dev, slot->host, bytes, hipMemcpyHostToDevice, ctx->compute);
     if (e == hipSuccess && record) e = hipEventRecord(slot->copied, ctx->compute);
     if (e != hipSuccess) {
       // The group's event may now be missing for this round: drain the stream
@@ -394,8 +417,7 @@ int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool 
       (void)hipStreamSynchronize(ctx->compute);
       return hip_fail(ctx, e, "job table upload");
     }
-    t.jobs = reinterpret_cast<const ltxw::JobDev*>(slot->dev);
-    t.begins = reinterpret_cast<const int64_t*>((char*)slot->dev + off_b);
+    t.table = slot->dev;
   }
   HIP_TRY(ctx, ltxw::launch_fused(t, f32out, multi, fdt, base16, ctx->compute), "fused kernel launch");
   return LTXW_OK;

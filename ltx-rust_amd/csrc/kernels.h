@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 namespace ltxw {
@@ -67,14 +68,42 @@ struct JobDev {
   StepDev step[kMaxSteps];
 };
 
-struct JobTable {
-  JobDev one;            // used when n_jobs == 1 (no device table needed)
-  const JobDev* jobs;    // device array when n_jobs > 1
-  const int64_t* begins; // device array of unit_begin, ascending
-  int32_t n_jobs;
-  int64_t total_units;   // workgroups in the launch
-  int32_t lds_ld;        // AT row stride (bf16): 8 + the launch's largest total padded rank
+// One tensor of a fused launch as the fused kernels read it: this header,
+// then one StepDev per K-step of the launch (record bytes
+// sizeof(FusedJob) + KS * sizeof(StepDev), a multiple of 16). Built from a
+// JobDev by the host (plan_fused fills the fields it copies).
+struct FusedJob {
+  const uint8_t* w;
+  void* out;
+  const float* scales;
+  uint32_t rows, cols, bands_n;
+  uint32_t unit_begin;  // first workgroup of this job in the launch
+  uint32_t fmt, scale_mode, qmask, cmul;
+  float coeff_out;
+  uint32_t pad;
 };
+static_assert(sizeof(FusedJob) == 64 && sizeof(StepDev) == 32, "record layout");
+
+// Kernel arguments of a fused launch. The job records travel in the kernel
+// arguments themselves (`inl`, read by the kernel from its argument segment)
+// when they fit, so a grouped launch of a DiT block needs no table upload;
+// larger launches read them from device memory (`table`).
+constexpr int kInlineTableBytes = 2944;
+constexpr int kInlineBegins = 16;
+struct JobTable {
+  JobDev one;            // the job of a one-job launch (n_jobs == 1)
+  const void* table;     // device records; nullptr: the records are in `inl`
+  int32_t n_jobs;
+  int32_t lds_ld;        // AT row stride (bf16): 8 + the launch's largest total padded rank
+  int64_t total_units;   // workgroups in the launch
+  int32_t rec_bytes;     // bytes per job record: sizeof(FusedJob) + K-steps * sizeof(StepDev)
+  int32_t pad[3];
+  // unit_begin of the inline records (n_jobs <= kInlineBegins; the rest
+  // UINT32_MAX), so that a workgroup finds its record with one load.
+  uint32_t begins[kInlineBegins];
+  alignas(16) unsigned char inl[kInlineTableBytes];
+};
+static_assert(sizeof(JobTable) <= 4096, "kernel arguments of a fused launch");
 
 struct DequantArgs {
   const uint8_t* w;

@@ -358,7 +358,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 3
   extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
   const int tid = threadIdx.x;
   const uint32_t pair = xcd_remap(blockIdx.x, gridDim.x);
-  const PJ J = pj_load(tab, pair);
+  const PJ J = pj_load<KS>(tab, pair);
   const uint32_t p = pair - J.unit_begin;
   const uint32_t i0 = (p % J.bands_n) * kBandCols;
   const uint32_t gA = (p / J.bands_n) * (2 * kWavesPerGroup * kStripRows);

@@ -174,23 +174,50 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t n) {
 // while the HBM data is still in flight. (Single-LoRA launches of at most
 // kWFirstMaxGrid workgroups request the first unit's FP8 bytes first.)
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void load_job(const JobTable& t, uint64_t unit, JobDev& J) {
-  if (t.n_jobs == 1) {
-    J = t.one;
-    return;
-  }
-  int lo = 0, hi = t.n_jobs - 1;  // last job with begins[j] <= unit
-  while (lo < hi) {
-    int mid = (lo + hi + 1) >> 1;
-    if ((uint64_t)G(t.begins)[mid] <= unit) lo = mid; else hi = mid - 1;
-  }
-  // Copy the descriptor as 16-byte global loads (the table is 256-byte aligned).
-  static_assert(sizeof(JobDev) % 16 == 0, "JobDev is copied in 16-byte pieces");
-  u32x4 raw[sizeof(JobDev) / 16];
-  const auto src = G(reinterpret_cast<const u32x4*>(t.jobs + lo));
+// Job records are read with scalar loads through constant-address-space
+// pointers, from the kernel's argument segment (records inline in the
+// JobTable argument) or from the device table. Both are read-only for the
+// launch's lifetime.
+using CByte = const __attribute__((address_space(4))) unsigned char;
+template <typename T>
+__device__ __forceinline__ T kload(CByte* p) {
+  static_assert(sizeof(T) % 4 == 0, "whole dwords");
+  struct Raw {
+    uint32_t w[sizeof(T) / 4];
+  } r;
 #pragma unroll
-  for (int k = 0; k < (int)(sizeof(JobDev) / 16); ++k) raw[k] = src[k];
-  __builtin_memcpy(&J, raw, sizeof(JobDev));
+  for (int k = 0; k < (int)(sizeof(T) / 4); ++k)
+    r.w[k] = *reinterpret_cast<const __attribute__((address_space(4))) uint32_t*>(p + 4 * k);
+  return __builtin_bit_cast(T, r);
+}
+
+// The record of the job that owns workgroup `wg`: the last one whose
+// unit_begin is <= wg (records in ascending unit_begin). Inline tables of up
+// to kInlineBegins jobs: a count over JobTable::begins (one load, no
+// dependent search); device tables: a binary search over the records.
+template <int KS>
+__device__ __forceinline__ CByte* job_record(const JobTable& t, uint32_t wg) {
+  constexpr uint32_t S = sizeof(FusedJob) + KS * sizeof(StepDev);
+  CByte* karg = (CByte*)__builtin_amdgcn_kernarg_segment_ptr();
+  if (!t.table && t.n_jobs <= kInlineBegins) {
+    uint32_t idx = 0;
+#pragma unroll
+    for (int j = 1; j < kInlineBegins; ++j) idx += t.begins[j] <= wg ? 1u : 0u;
+    return karg + offsetof(JobTable, inl) + idx * S;
+  }
+  CByte* base = t.table ? (CByte*)(uint64_t)t.table : karg + offsetof(JobTable, inl);
+  uint32_t lo = 0, hi = (uint32_t)t.n_jobs - 1;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi + 1) >> 1;
+    if (kload<uint32_t>(base + mid * S + offsetof(FusedJob, unit_begin)) <= wg) lo = mid;
+    else hi = mid - 1;
+  }
+  return base + lo * S;
+}
+
+template <int KS>
+__device__ __forceinline__ StepDev job_step(CByte* rec, int s) {
+  return kload<StepDev>(rec + sizeof(FusedJob) + s * sizeof(StepDev));
 }
 
 // Loads and stores at a 32-bit byte offset from a wave-uniform base pointer,
@@ -241,27 +268,49 @@ struct PJ {
   float tscale;   // the per-tensor scale (scale_mode 1), else 1
 };
 
-__device__ __forceinline__ PJ pj_load(const JobTable& t, uint64_t unit) {
-  JobDev J;
-  load_job(t, unit, J);
+template <int KS>
+__device__ __forceinline__ PJ pj_load(const JobTable& t, uint32_t wg) {
   PJ p;
-  p.w = uni_ptr(J.w);
-  p.out = uni_ptr(J.out);
-  p.scales = uni_ptr(J.scales);
-  p.a = uni_ptr(J.lora[0].a);
-  p.b = uni_ptr(J.lora[0].b);
-  p.rows = uni((uint32_t)J.rows);
-  p.cols = uni((uint32_t)J.cols);
-  p.rank = uni((uint32_t)J.lora[0].rank);
-  p.bands_n = uni((uint32_t)J.bands_n);
-  p.scale_mode = uni((uint32_t)J.scale_mode);
-  p.fmt = uni((uint32_t)J.fmt);
+  if (t.n_jobs == 1) {
+    // One-job launches read their JobDev, which sits at a fixed place in
+    // the kernel arguments (its loads go out with the launch header's).
+    const JobDev& J = t.one;
+    p.w = uni_ptr(J.w);
+    p.out = uni_ptr(J.out);
+    p.scales = uni_ptr(J.scales);
+    p.a = uni_ptr(J.lora[0].a);
+    p.b = uni_ptr(J.lora[0].b);
+    p.rows = uni((uint32_t)J.rows);
+    p.cols = uni((uint32_t)J.cols);
+    p.rank = uni((uint32_t)J.lora[0].rank);
+    p.bands_n = uni((uint32_t)J.bands_n);
+    p.scale_mode = uni((uint32_t)J.scale_mode);
+    p.fmt = uni((uint32_t)J.fmt);
+    p.coeff = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.coeff_out)));
+    p.cmul = uni(J.cmul);
+    p.unit_begin = uni((uint32_t)J.unit_begin);
+  } else {
+    CByte* rec = job_record<KS>(t, wg);
+    const FusedJob J = kload<FusedJob>(rec);
+    const StepDev s0 = job_step<KS>(rec, 0);  // step 0 starts at the LoRA's B and A
+    p.w = J.w;
+    p.out = J.out;
+    p.scales = J.scales;
+    p.a = reinterpret_cast<const uint16_t*>(s0.a);
+    p.b = reinterpret_cast<const uint16_t*>(s0.b);
+    p.rows = J.rows;
+    p.cols = J.cols;
+    p.rank = s0.rank;
+    p.bands_n = J.bands_n;
+    p.scale_mode = J.scale_mode;
+    p.fmt = J.fmt;
+    p.coeff = J.coeff_out;
+    p.cmul = J.cmul;
+    p.unit_begin = J.unit_begin;
+  }
   // One uniform load at the start: no per-lane load in the scale branch of
   // the factor issue (a vector load on one path only costs waits on both).
-  p.tscale = p.scale_mode == 1 ? *G(uni_ptr(J.scales)) : 1.0f;
-  p.coeff = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.coeff_out)));
-  p.cmul = uni(J.cmul);
-  p.unit_begin = uni((uint32_t)J.unit_begin);
+  p.tscale = p.scale_mode == 1 ? *G(uni_ptr(p.scales)) : 1.0f;
   return p;
 }
 

@@ -77,39 +77,39 @@ struct PJM {
 };
 
 template <int KS, bool BSW>
-__device__ __forceinline__ PJM<KS> pjm_load(const JobTable& t, uint64_t unit) {
-  JobDev J;
-  load_job(t, unit, J);
+__device__ __forceinline__ PJM<KS> pjm_load(const JobTable& t, uint32_t wg) {
+  CByte* rec = job_record<KS>(t, wg);
+  const FusedJob J = kload<FusedJob>(rec);
   PJM<KS> m;
-  m.base.w = uni_ptr(J.w);
-  m.base.out = uni_ptr(J.out);
-  m.base.scales = uni_ptr(J.scales);
+  m.base.w = J.w;
+  m.base.out = J.out;
+  m.base.scales = J.scales;
   m.base.a = nullptr;
   m.base.b = nullptr;
-  m.base.rows = uni((uint32_t)J.rows);
-  m.base.cols = uni((uint32_t)J.cols);
+  m.base.rows = J.rows;
+  m.base.cols = J.cols;
   m.base.rank = 0;
-  m.base.bands_n = uni((uint32_t)J.bands_n);
-  m.base.scale_mode = uni((uint32_t)J.scale_mode);
-  m.base.fmt = uni((uint32_t)J.fmt);
-  m.base.tscale = m.base.scale_mode == 1 ? *G(uni_ptr(J.scales)) : 1.0f;
-  m.base.coeff = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.coeff_out)));
-  m.base.cmul = uni(J.cmul);
-  m.base.unit_begin = uni((uint32_t)J.unit_begin);
+  m.base.bands_n = J.bands_n;
+  m.base.scale_mode = J.scale_mode;
+  m.base.fmt = J.fmt;
+  m.base.tscale = m.base.scale_mode == 1 ? *G(J.scales) : 1.0f;
+  m.base.coeff = J.coeff_out;
+  m.base.cmul = J.cmul;
+  m.base.unit_begin = J.unit_begin;
+  m.pf = 0;
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    m.a[s] = uni_ptr(J.step[s].a);
-    m.b[s] = uni_ptr(J.step[s].b);
-    m.rank[s] = uni(J.step[s].rank);
-    m.klim[s] = uni(J.step[s].klim);
-    m.q[s] = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.step[s].q)));
+    const StepDev st = job_step<KS>(rec, s);
+    m.a[s] = st.a;
+    m.b[s] = st.b;
+    m.rank[s] = st.rank;
+    m.klim[s] = st.klim;
+    m.q[s] = st.q;
+    if constexpr (BSW) {
+      if (s + 1 < KS) m.pf |= (st.pair & 1u) << s;
+    }
   }
-  m.qmask = uni(J.qmask);
-  m.pf = 0;
-  if constexpr (BSW) {
-#pragma unroll
-    for (int s = 0; s + 1 < KS; ++s) m.pf |= (uni(J.step[s].pair) & 1u) << s;
-  }
+  m.qmask = J.qmask;
   return m;
 }
 

@@ -357,6 +357,47 @@ def test_many_grouped_calls_in_flight(ctx):
             d.free()
 
 
+def test_grouped_calls_with_device_job_tables(ctx):
+    """Grouped launches whose job records do not fit the kernel arguments
+    (30 single-LoRA jobs; 14 jobs with two LoRAs, 5 K-steps) read them from
+    the device table ring: 24 calls queued without a wait reuse every slot.
+    Every output must equal the tensor's own single-call result."""
+    log("case: grouped calls with device job tables")
+    cases = [synth.tensor_case(5000 + k, 256, 256, synth.E4M3FN, synth.SCALE_ROW, loras=((64, 1.0),))
+             for k in range(30)]
+    cases += [synth.tensor_case(5100 + k, 130, 264, synth.E5M2, synth.SCALE_TENSOR, loras=((32, 1.0), (128, 0.5)))
+              for k in range(14)]
+    devs = [U.Dev(ctx, c) for c in cases]
+    outs = []
+    try:
+        singles = []
+        for d in devs:
+            d.run()
+            singles.append(d.result())
+        n_calls = 24
+        outs = [[ctx.alloc(d.n * d.ob) for d in devs] for _ in range(n_calls)]
+        for call in outs:
+            for o, d in zip(call, devs):
+                ctx.memset(o, 0xFF, d.n * d.ob)
+        ctx.synchronize()
+        for call in outs:
+            ctx.grouped([{"w": d.w, "out": o, "scales": d.s, "rows": d.case["rows"], "cols": d.case["cols"],
+                          "fmt": d.case["fmt"], "scale_mode": d.case["scale_mode"], "loras": d.loras}
+                         for o, d in zip(call, devs)])
+        ctx.synchronize()
+        for k, call in enumerate(outs):
+            for o, d, s in zip(call, devs, singles):
+                got = np.empty_like(s)
+                ctx.download(o, got)
+                assert np.array_equal(got, s), "call %d" % k
+    finally:
+        for call in outs:
+            for o in call:
+                ctx.free(o)
+        for d in devs:
+            d.free()
+
+
 def test_grouped_block_matches_single_calls(ctx):
     """A grouped launch over mixed tensors equals per-tensor calls bit for bit."""
     log("case: grouped vs single")
