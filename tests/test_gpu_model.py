@@ -11,7 +11,8 @@ sampled rows and the A factors are read), so the check covers the staging
 pipeline, the key rules and the merge bookkeeping as well as the kernels.
 Bar: gpu_util.compare_lora_bf16 on every tensor (1 bf16 ulp of the
 reference's result, or no farther from the exact value than the
-reference's own f32; Frobenius <= 1e-3).
+reference's own f32, or for an ill-conditioned element the f32
+forward-error bound; Frobenius <= 1e-3).
 """
 import os
 import sys
