@@ -444,12 +444,14 @@ class Lead:
     """Large streaming-dequant launches queued on the compute stream just
     before a timed region, so that the timed launches queue up behind them
     and run back to back even when the host submits them slower than the GPU
-    runs them (a profiler's per-launch cost). 2^28 FP8 elements of random
-    non-NaN codes per launch (about 0.15 ms); not part of any timed figure
-    except the streaming ceiling, which times these launches themselves."""
+    runs them (a profiler's per-launch cost). 2^30 FP8 elements of random
+    non-NaN codes per launch (a 64 MiB random block repeated; about 0.55 ms
+    per launch, so few launches cover a long submission); not part of any
+    timed figure except the streaming ceiling, which times these launches
+    themselves."""
 
-    N = 1 << 28
-    LAUNCH_US = 150.0
+    N = 1 << 30
+    LAUNCH_US = 550.0
 
     def __init__(self, ctx):
         import ltx_weights as lw
@@ -459,16 +461,16 @@ class Lead:
         self.out = ctx.alloc(2 * self.N)
         self.s = ctx.alloc(4)
         rng = np.random.default_rng(7)
-        chunk = 1 << 24
-        for off in range(0, self.N, chunk):
-            codes = rng.integers(0, 0x7F, size=chunk, dtype=np.uint8)  # 0x7F / 0xFF are the NaNs
-            codes |= (rng.integers(0, 2, size=chunk, dtype=np.uint8) << 7)
+        block = 1 << 26
+        codes = rng.integers(0, 0x7F, size=block, dtype=np.uint8)  # 0x7F / 0xFF are the NaNs
+        codes |= rng.integers(0, 2, size=block, dtype=np.uint8) << 7
+        for off in range(0, self.N, block):
             ctx.upload(codes, self.w + off)
         ctx.upload(np.array([0.5], np.float32), self.s)
 
     def launch(self, n):
         for _ in range(n):
-            self.ctx.dequant(self.w, self.N >> 12, 4096, self.lw.FMT_E4M3FN, self.lw.SCALE_TENSOR, self.s, self.out)
+            self.ctx.dequant(self.w, self.N >> 14, 1 << 14, self.lw.FMT_E4M3FN, self.lw.SCALE_TENSOR, self.s, self.out)
 
     def queue(self, host_us):
         """Enough launches to cover host_us of host-side submission."""
@@ -478,9 +480,9 @@ class Lead:
         """n device-to-device copies of 256 MiB (the first half of the output
         buffer into the second): the known-size dispatches that the HBM
         counters of a profiled run are scaled by."""
-        half = self.N
+        size = 1 << 28
         for _ in range(n):
-            hip.copy_d2d(self.out + half, self.out, half, stream)
+            hip.copy_d2d(self.out + size, self.out, size, stream)
 
     def free(self):
         for p in (self.w, self.out, self.s):
@@ -489,7 +491,7 @@ class Lead:
 
 def stream_ceiling(ctx, hip, stream, lead, reps=20):
     """The library's streaming dequant (16 FP8 bytes in, 32 bytes of bf16 out
-    per thread) over 2^28 elements: the 1 B in / 2 B out pattern with no tile
+    per thread) over 2^30 elements: the 1 B in / 2 B out pattern with no tile
     structure, the ceiling the fused kernels' traffic is compared with. `reps`
     launches timed back to back behind a queued lead."""
     lead.queue(reps * 20.0)
@@ -499,7 +501,7 @@ def stream_ceiling(ctx, hip, stream, lead, reps=20):
     hip.record(e1, stream)
     us = hip.elapsed_ms(e0, e1) * 1e3 / reps
     gbps = (3.0 * Lead.N + 4) / (us * 1e-6) / 1e9
-    return {"kernel": "k_dequant (ltxw_dequant, 2^28 random e4m3fn codes, one scale, bf16 out)",
+    return {"kernel": "k_dequant (ltxw_dequant, 2^30 e4m3fn codes, a 64 MiB random block repeated, one scale, bf16 out)",
             "us": round(us, 2), "GBps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4), "launches": reps}
 
 
@@ -527,7 +529,7 @@ def kernel_config(name, ctx, hip, stream, lead, steps, warmup, exact=False, chec
             ctx.grouped(descs[k % n_inst])
         ctx.synchronize()
         # Queue ahead of the timed launches (see Lead), then time them.
-        lead.queue(steps * 40.0)
+        lead.queue(steps * 50.0)
         t_start, t_end = hip.event(), hip.event()
         hip.record(t_start, stream)
         h0 = time.perf_counter()

@@ -28,9 +28,11 @@ def ctx():
 
 
 def tensor_set(seed, big):
-    """Descriptor specs: several single-LoRA jobs (one fused launch with a job
-    table), several two-LoRA jobs (the several-LoRA kernel's table), f32
-    outputs, a plain dequant and a reference-order (exact) tensor."""
+    """Descriptor specs: several single-LoRA jobs, several two-LoRA jobs (the
+    several-LoRA kernel), f32 outputs, a plain dequant, a reference-order
+    (exact) tensor, and enough small rank-64 tensors (30, or 25 in the small
+    set) that their launch's job records exceed what the kernel arguments
+    carry, so that launch reads them from the scratch array."""
     s = 2 if big else 1
     specs = [
         (256 * s, 512 * s, ((64, 1.0),), lw.OUT_BF16, 0),
@@ -45,6 +47,7 @@ def tensor_set(seed, big):
     ]
     if not big:
         specs = specs[1:5] + specs[6:8]
+    specs += [(64 + 8 * (k % 3), 128, ((64, 1.0),), lw.OUT_BF16, 0) for k in range(30 if big else 25)]
     cases = []
     for k, (rows, cols, loras, out_dtype, flags) in enumerate(specs):
         fmt = synth.E5M2 if k % 3 == 1 else synth.E4M3FN
