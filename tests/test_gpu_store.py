@@ -524,6 +524,73 @@ def test_dlpack_export_of_materialised_tensor(ctx, tmp):
         t.free()
 
 
+def test_materialised_weight_consumed_in_place_by_rocblas_gemm(ctx, tmp):
+    """The hand-off to a consumer: rocBLAS (the system ROCm runtime, as a
+    Burn HIP backend would use) runs y = x W^T straight on the bf16 buffer
+    that materialize wrote, through the DLPack capsule's data pointer and on
+    the library's compute stream, as ltx-dit's load_linear transposes the
+    [out, in] weight (crates/ltx-dit/src/load.rs:149-170) and multiplies.
+    The GEMM's f32 output must match the f64 product of the same bf16
+    weights within the f32 GEMM error bound."""
+    from ltx_weights import _dlpack
+    log("hand-off: rocBLAS GEMM on the materialised buffer")
+    try:
+        rb = ctypes.CDLL("librocblas.so")
+    except OSError:
+        pytest.skip("librocblas.so not found")
+    rows, cols, batch = 384, 1024, 16
+    case = synth.tensor_case(77, rows, cols, synth.E4M3FN, synth.SCALE_ROW, loras=((64, 1.0),))
+    b, a, r, c = case["loras"][0]
+    store = WeightStore.open([tmp([("l.weight", "F8_E4M3", [rows, cols], case["w"]),
+                                   ("l.weight_scale", "F32", [rows], case["scales"])])])
+    store.merge_lora(LoraFile.open(tmp([("l.lora_A.weight", "BF16", [r, cols], a),
+                                        ("l.lora_B.weight", "BF16", [rows, r], b)])), c)
+    t = store.materialize_bf16(ctx, ["l.weight"])["l.weight"]
+    rng = np.random.default_rng(5)
+    x = synth.bf16_from_f64(rng.normal(0.0, 1.0, size=(batch, cols)))
+    px = ctx.alloc(x.nbytes)
+    py = ctx.alloc(batch * rows * 4)
+    handle = ctypes.c_void_p()
+    try:
+        cap = t.__dlpack__()  # held until the consumer's release below
+        mt = _dlpack.view(cap)
+        w_ptr = mt.dl_tensor.data
+        ctx.upload(x, px)
+        vp = ctypes.c_void_p
+        rb.rocblas_create_handle.argtypes = [ctypes.POINTER(vp)]
+        rb.rocblas_set_stream.argtypes = [vp, vp]
+        rb.rocblas_destroy_handle.argtypes = [vp]
+        i32 = ctypes.c_int
+        rb.rocblas_gemm_ex.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp, i32, i32, vp, i32, i32, vp, vp, i32, i32,
+                                       vp, i32, i32, i32, i32, ctypes.c_int32, ctypes.c_uint32]
+        assert rb.rocblas_create_handle(ctypes.byref(handle)) == 0
+        assert rb.rocblas_set_stream(handle, ctx.stream()) == 0
+        alpha, beta = ctypes.c_float(1.0), ctypes.c_float(0.0)
+        none, trans, bf16, f32_ = 111, 112, 168, 151
+        # Column-major view: Y^T [rows x batch] = W [rows x cols] * X^T [cols x batch]; the
+        # row-major [rows, cols] weight is the column-major [cols x rows] matrix W^T.
+        st = rb.rocblas_gemm_ex(handle, trans, none, rows, batch, cols, ctypes.byref(alpha), w_ptr, bf16, cols,
+                                px, bf16, cols, ctypes.byref(beta), py, f32_, rows, py, f32_, rows, f32_, 0, 0, 0)
+        assert st == 0, f"rocblas_gemm_ex status {st}"
+        ctx.synchronize()
+        y = np.empty((batch, rows), np.float32)
+        ctx.download(py, y)
+        w64 = U.bf16_to_f64(t.to_numpy())
+        x64 = U.bf16_to_f64(x)
+        ref = x64 @ w64.T
+        bound = (cols + 2) * 2.0 ** -24 * (np.abs(x64) @ np.abs(w64).T)
+        assert np.all(np.abs(y - ref) <= bound), float(np.max(np.abs(y - ref) / np.maximum(bound, 1e-300)))
+        # and the weight the GEMM read is the library's result
+        U.compare_lora_bf16(case, t.to_numpy())
+        mt.deleter(ctypes.pointer(mt))
+    finally:
+        if handle.value:
+            rb.rocblas_destroy_handle(handle)
+        ctx.free(px)
+        ctx.free(py)
+        t.free()
+
+
 def test_exact_materialise_of_synthetic_block(ctx, tmp_path):
     """LTXW_MAT_EXACT: a DiT block (two stacked bf16 LoRAs, mixed formats)
     bit-identical to the reference order on sampled rows."""
