@@ -215,7 +215,6 @@ __device__ __forceinline__ CByte* job_record(const JobTable& t, uint32_t wg) {
   return base + lo * S;
 }
 
-template <int KS>
 __device__ __forceinline__ StepDev job_step(CByte* rec, int s) {
   return kload<StepDev>(rec + sizeof(FusedJob) + s * sizeof(StepDev));
 }
@@ -292,7 +291,7 @@ __device__ __forceinline__ PJ pj_load(const JobTable& t, uint32_t wg) {
   } else {
     CByte* rec = job_record<KS>(t, wg);
     const FusedJob J = kload<FusedJob>(rec);
-    const StepDev s0 = job_step<KS>(rec, 0);  // step 0 starts at the LoRA's B and A
+    const StepDev s0 = job_step(rec, 0);  // step 0 starts at the LoRA's B and A
     p.w = J.w;
     p.out = J.out;
     p.scales = J.scales;

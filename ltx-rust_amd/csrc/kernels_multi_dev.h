@@ -99,7 +99,7 @@ __device__ __forceinline__ PJM<KS> pjm_load(const JobTable& t, uint32_t wg) {
   m.pf = 0;
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    const StepDev st = job_step<KS>(rec, s);
+    const StepDev st = job_step(rec, s);
     m.a[s] = st.a;
     m.b[s] = st.b;
     m.rank[s] = st.rank;
