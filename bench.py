@@ -130,6 +130,32 @@ def cpu_baseline(case, budget_s, threads=None):
     return threads, reps, dt
 
 
+def cpu_config(cases, threads):
+    """The oracle over one step of a workload: every tensor once on `threads`
+    host threads, and the first tensor on one thread (extrapolated to the
+    step by algorithmic bytes). Returns the figures for the bench line."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+
+    def run(c, th):
+        loras = [(b, a, O.BF16, co) for (b, a, r, co) in c["loras"]]
+        fmt = O.E4M3FN if c["fmt"] == 0 else O.E5M2
+        O.read_bf16(c["w"], fmt, c["scale_mode"], c["scales"], loras, threads=th)
+
+    step_bytes = sum(synth_bytes(c) for c in cases)
+    t0 = time.perf_counter()
+    for c in cases:
+        run(c, threads)
+    dt = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    run(cases[0], 1)
+    dt1 = (time.perf_counter() - t0) * step_bytes / synth_bytes(cases[0])
+    return {"GBps": round(step_bytes / dt / 1e9, 3), "s_per_step": round(dt, 4), "threads": threads,
+            "GBps_1_thread": round(step_bytes / dt1 / 1e9, 3), "s_per_step_1_thread": round(dt1, 3),
+            "sample": f"every tensor of one step once on {threads} threads; one thread on the first tensor "
+                      f"({cases[0]['rows']}x{cases[0]['cols']}), extrapolated to the step by algorithmic bytes"}
+
+
 def workload_cases(name, synth):
     """The tensors one step materialises, as synth.tensor_case dicts."""
     if name == "layer":
@@ -647,9 +673,10 @@ def main():
     value = head["GBps"]
     configs = {CONFIG_OF.get(args.workload, args.workload): dict(head, name=args.workload)}
     csteps = args.config_steps or max(args.steps, 20)
+    config_cases = {}
     for name in extra:
         r = kernel_config(name, ctx, hip, stream, lead, csteps, min(args.warmup, 5) or 1)
-        r.pop("_cases")
+        config_cases[name] = r.pop("_cases")
         configs[CONFIG_OF.get(name, name)] = dict(r, name=name)
     ceiling = stream_ceiling(ctx, hip, stream, lead) if default_run else None
     if ceiling:
@@ -677,6 +704,12 @@ def main():
         _, reps1, dt1 = cpu_baseline(c0, min(5.0, args.cpu_seconds / 2), threads=1)
         cpu["value_1_thread"] = round(b0 * reps1 / dt1 / 1e9, 3)
         cpu["s_per_tensor_1_thread"] = round(dt1 / reps1, 4)
+        # The other kernel workloads, one step each (reported beside their GPU figures).
+        for name, cc in config_cases.items():
+            log(f"cpu baseline: {name}")
+            k = CONFIG_OF.get(name, name)
+            configs[k]["cpu"] = cpu_config(cc, threads)
+            configs[k]["gpu_over_cpu"] = round(configs[k]["GBps"] / configs[k]["cpu"]["GBps"], 1)
 
     e2e = {}
     for run in e2e_runs:
