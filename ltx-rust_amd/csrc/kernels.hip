@@ -376,11 +376,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 3
 
 // ---------------------------------------------------------------------------
 // (a') Tiled dequant: the fused kernels' tile walk and lane layout without
-// the LoRA. A workgroup takes two vertically adjacent 128 x 128 units of a
-// column band; lane l of wave w handles, in each unit, the 8 columns
-// i0 + 8 (l % 16) .. +7 of rows r0 + 4 (l / 16) + {0..3, 16..19} with
-// r0 = g0 + 32 w. Both units' bytes are requested before the first unit is
-// converted. Faster than the streaming kernel up to an FFN matrix
+// the LoRA. A workgroup takes U (1, 2 or 4) vertically adjacent 128 x 128
+// units of a column band; lane l of wave w handles, in each unit, the 8
+// columns i0 + 8 (l % 16) .. +7 of rows r0 + 4 (l / 16) + {0..3, 16..19}
+// with r0 = g0 + 32 w. Every unit's bytes are requested before the first
+// unit is converted. Faster than the streaming kernel up to an FFN matrix
 // (4096 x 4096: 9.2 against 11.5 us; 16384 x 4096: 37.8 against 38.7 us with
 // the streaming kernel at its best setting).
 // ---------------------------------------------------------------------------
