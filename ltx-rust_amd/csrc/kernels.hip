@@ -315,7 +315,13 @@ __global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
 
 // Two vertically adjacent units of one band (rows [gA, gA + 256)).
 // WFIRST (launches of at most kWFirstMaxGrid workgroups): the first unit's
-// FP8 bytes are requested before the factors.
+// FP8 bytes are requested before the factors, and the second unit's factor
+// fragments go out during the first unit's epilogue. Larger launches of 2
+// K-steps and more request both units' factors before any FP8 bytes (loads
+// complete in issue order, so the second unit's LoRA product then never
+// waits for FP8 bytes); the registers this takes leave two waves per SIMD
+// (DiT block 153.0 -> 150.2 us, rank-128 mixed-format block -2%; with one
+// K-step the third wave per SIMD is worth more, +1.4%).
 template <bool F32OUT, int KS, int FMT, bool FULL, bool BSW, bool WFIRST>
 __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i0, uint32_t gA, uint32_t gB,
                                            bool hasB, int tid) {
@@ -329,6 +335,7 @@ __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i
   } else {
     pp_issue_a<KS>(J, i0, tid, st);
     pp_issue_f<KS, FULL, BSW>(J, i0, gA, tid, fa);
+    if constexpr (KS >= 2) pp_issue_f<KS, FULL, BSW>(J, i0, hasB ? gB : gA, tid, fb);
     pp_issue_w<KS, FULL>(J, i0, gA, tid, fa);
   }
   pp_issue_w<KS, FULL>(J, i0, hasB ? gB : gA, tid, fb);
@@ -337,7 +344,7 @@ __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i
   {
     Acc<KS> acc;
     pp_mfma<KS, BSW>(J, fa, AT, LD, tid, acc);
-    pp_issue_f<KS, FULL, BSW>(J, i0, hasB ? gB : gA, tid, fb);
+    if constexpr (WFIRST || KS == 1) pp_issue_f<KS, FULL, BSW>(J, i0, hasB ? gB : gA, tid, fb);
     pp_epilogue<F32OUT, KS, FULL, FMT>(J, fa, acc, i0, gA, tid);
   }
   // Re-read the A^T fragments for the second unit rather than keeping them
@@ -354,7 +361,7 @@ __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i
 // B-fragment pair swap (launches of kSwapMinGrid workgroups and more);
 // WFIRST: FP8 bytes before factors (launches of at most kWFirstMaxGrid).
 template <bool F32OUT, int KS, bool BSW, bool WFIRST>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 3 : 2))) void k_fused_pair(JobTable tab) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS == 1 || (KS == 2 && WFIRST) ? 3 : 2))) void k_fused_pair(JobTable tab) {
   extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
   const int tid = threadIdx.x;
   const uint32_t pair = xcd_remap(blockIdx.x, gridDim.x);
