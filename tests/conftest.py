@@ -16,13 +16,14 @@ def pytest_configure(config):
 
 def pytest_sessionfinish(session, exitstatus):
     """Write the per-call statistics of the LoRA tolerance check (max ulp
-    distance, elements beyond 1 ulp, Frobenius errors) of a GPU session to
-    gpurun_out/parity_stats.json, when that directory exists."""
+    distance, elements beyond 1 ulp, ill-conditioned elements, Frobenius
+    errors) of a GPU session to the JSON file named by LTXW_PARITY_STATS,
+    when that variable is set."""
     gu = sys.modules.get("gpu_util")
-    out_dir = os.path.join(ROOT, "gpurun_out")
-    if gu is None or not getattr(gu, "STATS", None) or not os.path.isdir(out_dir):
+    path = os.environ.get("LTXW_PARITY_STATS")
+    if gu is None or not getattr(gu, "STATS", None) or not path:
         return
     import json
 
-    with open(os.path.join(out_dir, "parity_stats.json"), "w") as f:
+    with open(path, "w") as f:
         json.dump(gu.STATS, f, indent=0)
