@@ -642,8 +642,8 @@ def main():
                     help="LoRA deltas in the reference's operation order (LTXW_DESC_EXACT, bit-identical)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(the weight set shards by tensor with no exchange; see the design notes).", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the weight set shards by tensor with no exchange between GPUs).", file=sys.stderr)
         sys.exit(2)
 
     if args.workload in MODEL_WORKLOADS:

@@ -1,7 +1,8 @@
 /*
  * CPU oracle for the FP8 dequantisation + LoRA-merge read path.
  * TEST INFRASTRUCTURE ONLY: loaded by tests/, the smoke entry point and the
- * bench's CPU-baseline leg as the checker; never part of the product.
+ * bench's CPU-baseline leg as the reference the HIP path is compared with;
+ * never part of the product.
  *
  * Each function cites the reference file:line whose arithmetic it restates.
  * Compile without -ffast-math (signed zeros, NaN and fma must stay IEEE).

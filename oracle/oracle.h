@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the FP8 dequantisation + LoRA-merge read path.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker: tests/, the smoke
+ * TEST INFRASTRUCTURE ONLY. This library is the oracle: tests/, the smoke
  * entry point and the bench's CPU-baseline leg may load it; the product
  * (libltxw) never links, loads or calls it.
  *

@@ -1,6 +1,6 @@
 """ctypes binding of the CPU oracle (oracle/_build/liboracle.so).
 
-Test infrastructure: the checker that the HIP path is compared against.
+Test infrastructure: the oracle that the HIP path is compared against.
 """
 import ctypes
 import os
