@@ -720,7 +720,7 @@ def main():
                           host_threads=args.host_threads, staging_mib=args.staging_mib,
                           staging_slots=args.staging_slots, cold=cold)
             if cpu is not None and "device_bytes" in r:
-                # The oracle's rate on this box applied to the model's device bytes.
+                # The oracle's rate on this host applied to the model's device bytes.
                 r["cpu_estimate_s"] = round(r["device_bytes"] / (cpu["value"] * 1e9), 1)
         except Exception as ex:  # reported in the line, never hides the kernel result
             r = {"error": f"{type(ex).__name__}: {ex}"}
