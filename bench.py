@@ -316,7 +316,7 @@ def drop_page_cache(paths):
 
 
 def run_model(name, reps, warmup, log_prefix="", host_threads=8, staging_mib=0, staging_slots=0, cold=False,
-              check_tensors=12):
+              check_tensors=12, mfma=False):
     """Whole-model materialisation: seeded FP8 checkpoint + LoRA files on
     disk, then per step: WeightStore.open (mmap, header parse, key rules) ->
     LoraFile.open + merge_lora -> materialize every linear into resident bf16
@@ -325,7 +325,7 @@ def run_model(name, reps, warmup, log_prefix="", host_threads=8, staging_mib=0, 
     before every step, so `open` -> sync includes reading them from storage."""
     import ltx_weights as lw
     from ltx_weights import synth
-    from ltx_weights.store import KeyMap, LoraFile, WeightStore
+    from ltx_weights.store import MAT_MFMA, KeyMap, LoraFile, WeightStore
 
     n_blocks, variant, loras, seed = MODEL_WORKLOADS[name]
     layout = synth.model_layout(n_blocks, variant)
@@ -378,7 +378,7 @@ def run_model(name, reps, warmup, log_prefix="", host_threads=8, staging_mib=0, 
                 store.merge_lora(lf, strength)
                 lf.close()
             t2 = time.perf_counter()
-            store.materialize(ctx, keys, outs, lw.OUT_BF16)
+            store.materialize(ctx, keys, outs, lw.OUT_BF16, MAT_MFMA if mfma else 0)
             t3 = time.perf_counter()
             ctx.synchronize()
             t4 = time.perf_counter()
@@ -423,12 +423,20 @@ def run_model(name, reps, warmup, log_prefix="", host_threads=8, staging_mib=0, 
             got = np.empty((len(rows), c), dtype=np.uint16)
             for q, o in enumerate(rows):
                 ctx.download(outs[i] + 2 * int(o) * c, got[q])
+            if not mfma:  # the reference's operation order: bit for bit
+                if not np.array_equal(got, U.oracle_bf16(case)):
+                    raise AssertionError(f"{key}: exact materialisation differs from the oracle")
+                continue
             stats = U.compare_lora_bf16(case, got)
             worst = max(worst, stats["max_ulp"])
             over += stats["n_over_1ulp"]
             cond += stats.get("n_cond", 0)
-        res["parity"] = {"tensors_checked": len(picks), "of_tensors": len(layout), "rows_per_tensor": 3,
-                         "max_ulp": worst, "n_over_1ulp": over, "n_cond": cond, "bar": PARITY_BAR}
+        res["parity"] = ({"tensors_checked": len(picks), "of_tensors": len(layout), "rows_per_tensor": 3,
+                          "bit_exact": True} if not mfma else
+                         {"tensors_checked": len(picks), "of_tensors": len(layout), "rows_per_tensor": 3,
+                          "max_ulp": worst, "n_over_1ulp": over, "n_cond": cond, "bar": PARITY_BAR})
+        res["kernels"] = ("MFMA LoRA products (LTXW_MAT_MFMA)" if mfma else
+                          "reference operation order (materialize's default), bit-identical")
         log(f"{log_prefix}parity ok on {len(picks)} sampled tensors, max {worst} ulp")
         ctx.free(arena)
         ctx.close()
@@ -443,7 +451,8 @@ def run_model(name, reps, warmup, log_prefix="", host_threads=8, staging_mib=0, 
 
 def main_model(args):
     res = run_model(args.workload, args.steps, args.warmup, host_threads=args.host_threads,
-                    staging_mib=args.staging_mib, staging_slots=args.staging_slots, cold=args.cold)
+                    staging_mib=args.staging_mib, staging_slots=args.staging_slots, cold=args.cold,
+                    mfma=args.mfma_materialise)
     line = {
         "metric": METRIC,
         "value": res.get("s"),
@@ -629,7 +638,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget (0 skips it)")
     ap.add_argument("--e2e", default="auto",
                     help="comma-separated whole-model runs beside the kernel workloads: model22b, model, "
-                         "model-mixed, model22b-cold (auto: all four beside the default layer workload; none)")
+                         "model-mixed, with -mfma (MFMA kernels) and/or -cold suffixes (auto: model22b, "
+                         "model22b-mfma, model, model-mixed, model22b-cold beside the default layer workload; none)")
     ap.add_argument("--e2e-steps", type=int, default=3)
     ap.add_argument("--cold", action="store_true", help="whole-model workloads: evict the files' pages first")
     ap.add_argument("--host-threads", type=int, default=8,
@@ -638,6 +648,9 @@ def main():
                     help="pinned staging slot size in MiB for whole-model runs (0: the library default, 64)")
     ap.add_argument("--staging-slots", type=int, default=0,
                     help="pinned staging slots for whole-model runs (0: the library default, 16)")
+    ap.add_argument("--mfma-materialise", action="store_true",
+                    help="whole-model runs: LoRA deltas on the MFMA kernels (LTXW_MAT_MFMA) instead of "
+                         "materialize's default reference order")
     ap.add_argument("--exact", action="store_true",
                     help="LoRA deltas in the reference's operation order (LTXW_DESC_EXACT, bit-identical)")
     args = ap.parse_args()
@@ -656,7 +669,7 @@ def main():
     else:
         extra = [c for c in args.configs.split(",") if c and c != args.workload]
     if args.e2e == "auto":
-        e2e_runs = ["model22b", "model", "model-mixed", "model22b-cold"] if default_run else []
+        e2e_runs = ["model22b", "model22b-mfma", "model", "model-mixed", "model22b-cold"] if default_run else []
     elif args.e2e == "none":
         e2e_runs = []
     else:
@@ -713,18 +726,23 @@ def main():
 
     e2e = {}
     for run in e2e_runs:
-        name, cold = (run[:-5], True) if run.endswith("-cold") else (run, False)
+        name, cold, mfma = run, False, False
+        if name.endswith("-cold"):
+            name, cold = name[:-5], True
+        if name.endswith("-mfma"):
+            name, mfma = name[:-5], True
         log(f"whole-model materialisation ({run})")
         try:
             r = run_model(name, args.e2e_steps if not cold else 2, 1 if not cold else 0, log_prefix="  ",
                           host_threads=args.host_threads, staging_mib=args.staging_mib,
-                          staging_slots=args.staging_slots, cold=cold)
+                          staging_slots=args.staging_slots, cold=cold, mfma=mfma)
             if cpu is not None and "device_bytes" in r:
                 # The oracle's rate on this host applied to the model's device bytes.
                 r["cpu_estimate_s"] = round(r["device_bytes"] / (cpu["value"] * 1e9), 1)
         except Exception as ex:  # reported in the line, never hides the kernel result
             r = {"error": f"{type(ex).__name__}: {ex}"}
-        e2e[run] = dict(r, workload=WORKLOAD_TEXT[name] + (" (cold page cache)" if cold else ""))
+        e2e[run] = dict(r, workload=WORKLOAD_TEXT[name] + (" (cold page cache)" if cold else "") +
+                        (" (MFMA kernels)" if mfma else ""))
 
     line = {
         "metric": METRIC,

@@ -127,19 +127,21 @@ void ltxw_report_free(ltxw_merge_report* r);
 int ltxw_store_n_deltas(const ltxw_store* s, const char* key);
 int ltxw_store_delta(const ltxw_store* s, const char* key, int index, int32_t* rank, float* coeff);
 
-/* Options of ltxw_store_materialize and ltxw_store_read. The two entry
- * points differ in their defaults:
- *   materialize: a `{key}_scale` with exactly shape[0] elements (shape[0] > 1,
- *     two or more dims) scales row o by element o (an extension: per-output-
- *     channel FP8 scales), any other scale tensor by its element 0; LoRA deltas
- *     go through the MFMA kernels where they take them (within 1 bf16 ulp of
- *     the reference's result).
- *   read: the reference's `read` exactly: every scale tensor scales by its
- *     element 0 (src/store.rs:498-508, :732-735; empty: 1.0) and the deltas run
- *     in the reference's operation order, so the f32 result is bit-identical.
- * LTXW_MAT_SCALE_FIRST / LTXW_MAT_EXACT select the reference's rules (no-ops
- * for read); LTXW_MAT_ROW_SCALES / LTXW_MAT_MFMA select the extensions (no-ops
- * for materialize). A rule and its opposite together are LTXW_ERR_INVALID_ARG. */
+/* Options of ltxw_store_materialize and ltxw_store_read.
+ * Scales: materialize scales row o by element o of a `{key}_scale` with
+ *   exactly shape[0] elements (shape[0] > 1, two or more dims; an extension:
+ *   per-output-channel FP8 scales) and by element 0 otherwise; read always by
+ *   element 0 (src/store.rs:498-508, :732-735; empty: 1.0).
+ *   LTXW_MAT_SCALE_FIRST selects the element-0 rule for materialize,
+ *   LTXW_MAT_ROW_SCALES the per-row rule for read.
+ * LoRA deltas: both run them in the reference's operation order by default
+ *   (bit-identical to the reference's f32, then RNE for bf16). Materialize is
+ *   bound by the host -> HBM copies, which hide these kernels (a 22B-parameter
+ *   set with rank-64 deltas: 0.425 s either way). LTXW_MAT_MFMA selects the
+ *   MFMA kernels where they take the tensor (within 1 bf16 ulp of the
+ *   reference's result but for ill-conditioned elements); LTXW_MAT_EXACT
+ *   states the default explicitly.
+ * A rule and its opposite together are LTXW_ERR_INVALID_ARG. */
 #define LTXW_MAT_SCALE_FIRST 1u
 #define LTXW_MAT_EXACT 2u
 #define LTXW_MAT_ROW_SCALES 4u
@@ -151,8 +153,7 @@ int ltxw_store_delta(const ltxw_store* s, const char* key, int index, int32_t* r
  * merged delta, as `read` (src/store.rs:479-521) computes it, rounded to
  * bf16 (RNE) or kept f32. Non-FP8 base tensors and >= 2-D shapes are
  * accepted; a key with deltas must be [out, in] (src/store.rs:767-779).
- * LoRA factors of every type `merge_lora` accepts are taken (bf16 on the
- * MFMA path, the others in the reference's order). A key merged with more
+ * LoRA factors of every type `merge_lora` accepts are taken. A key merged with more
  * than LTXW_MAX_LORAS deltas runs all of them in the reference's order, in
  * passes of up to LTXW_MAX_LORAS deltas through an f32 accumulator (for bf16
  * output a device scratch buffer of 4 bytes per element, kept by the context).
@@ -170,7 +171,7 @@ int ltxw_store_materialize(ltxw_store* s, ltxw_ctx* ctx, const char* const* keys
  * into host memory (n == numel), bit-identical to the reference's (element-0
  * scale rule, every merged delta in merge order and in the reference's
  * operation order). `flags` (LTXW_MAT_ROW_SCALES, LTXW_MAT_MFMA) opt into the
- * materialize extensions. Synchronous. */
+ * extensions. Synchronous. */
 int ltxw_store_read(ltxw_store* s, ltxw_ctx* ctx, const char* key, uint32_t flags, float* out, int64_t n);
 
 #ifdef __cplusplus

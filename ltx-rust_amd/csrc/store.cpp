@@ -834,7 +834,10 @@ int materialize(ltxw_store* s, ltxw_ctx* ctx, const char* const* keys, int64_t n
   if (out_dtype != LTXW_OUT_BF16 && out_dtype != LTXW_OUT_F32)
     return sfail(LTXW_ERR_INVALID_ARG, "invalid output dtype %d", out_dtype);
   if (int rc = check_flags(flags)) return rc;
-  // The extensions are materialize's defaults.
+  // Per-row scales are materialize's default; the deltas run in the
+  // reference's operation order unless the MFMA kernels are asked for (the
+  // host -> HBM copies hide either).
+  if (!(flags & LTXW_MAT_MFMA)) flags |= LTXW_MAT_EXACT;
   flags &= ~(LTXW_MAT_ROW_SCALES | LTXW_MAT_MFMA);
   // Resolve and check every key before any work is queued.
   std::vector<Plan> plans;

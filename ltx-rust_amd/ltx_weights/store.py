@@ -274,7 +274,9 @@ class WeightStore:
         return shape, out.reshape(shape)
 
     def materialize(self, ctx, keys, outs, out_dtype=N.OUT_BF16, flags=0):
-        """Into caller-owned device pointers outs[k] (numel(keys[k]) elements each)."""
+        """Into caller-owned device pointers outs[k] (numel(keys[k]) elements
+        each). Per-row scales; LoRA deltas in the reference's operation order
+        (bit-identical) unless `flags` has MAT_MFMA."""
         karr = (ctypes.c_char_p * max(1, len(keys)))(*[k.encode() for k in keys])
         oarr = (ctypes.c_void_p * max(1, len(outs)))(*outs)
         N.check_store(N.lib().ltxw_store_materialize(self.h, ctx.h, karr, len(keys), out_dtype, flags, oarr))

@@ -256,12 +256,18 @@ def test_fused_path_through_store(ctx, tmp):
     for k, (b, a, r, c) in enumerate(case["loras"]):
         store.merge_lora(LoraFile.open(tmp([("m.lora_A.weight", "BF16", [r, 512], a),
                                             ("m.lora_B.weight", "BF16", [256, r], b)])), c)
-    out = store.materialize_bf16(ctx, ["m.weight"])["m.weight"]
+    out = store.materialize_bf16(ctx, ["m.weight"], flags=MAT_MFMA)["m.weight"]
     try:
         stats = U.compare_lora_bf16(case, out.to_numpy())
     finally:
         out.free()
     log("fused via store:", stats)
+    # Without MAT_MFMA: the reference's operation order, bit for bit.
+    out = store.materialize_bf16(ctx, ["m.weight"])["m.weight"]
+    try:
+        assert np.array_equal(out.to_numpy(), U.oracle_bf16(case))
+    finally:
+        out.free()
     del rng
 
 
@@ -730,13 +736,19 @@ def test_16bit_base_fused_path(ctx, tmp, base_dt, ranks, shape):
     case = {"w": w.reshape(rows, cols), "scales": None, "rows": rows, "cols": cols, "scale_mode": O.SCALE_NONE,
             "fmt": {"BF16": lw.FMT_BF16, "F16": lw.FMT_F16}[base_dt],
             "loras": [(b, a, b.shape[1], c) for (b, a, c) in loras]}
-    out = store.materialize_bf16(ctx, ["t.weight"])["t.weight"]
+    out = store.materialize_bf16(ctx, ["t.weight"], flags=MAT_MFMA)["t.weight"]
     try:
         U.compare_lora_bf16(case, out.to_numpy())
     finally:
         out.free()
     want = O.read_bf16(case["w"], O.DTYPE_CODES[base_dt], O.SCALE_NONE, None,
                        [(b, a, O.BF16, c) for (b, a, c) in loras])
+    for flags in (0, MAT_EXACT):  # the default is the reference's order
+        out = store.materialize_bf16(ctx, ["t.weight"], flags=flags)["t.weight"]
+        try:
+            assert np.array_equal(out.to_numpy(), want)
+        finally:
+            out.free()
     out = store.materialize_bf16(ctx, ["t.weight"], flags=MAT_EXACT)["t.weight"]
     try:
         assert np.array_equal(out.to_numpy(), want)
