@@ -138,8 +138,21 @@ __device__ __forceinline__ float factor_at(const void* p, int dt, uint64_t e) {
   else return canon_nan(decode1(reinterpret_cast<const uint8_t*>(p)[e], FDT - 3));
 }
 
+// LDS slot of band column c in a staged A row: column 8q + 4h + j (q < 16,
+// h < 2, j < 4) sits at 64h + 4q + j. Thread cg's columns 8cg .. 8cg + 7 are
+// then the two 16-byte pieces at 4cg and 64 + 4cg, and the 16 lanes of one
+// piece read 256 contiguous bytes: no bank conflicts (with 8 contiguous
+// columns per lane, lanes cg and cg + 4 met in the same banks; rocprof's
+// SQ_LDS_BANK_CONFLICT fell 11x, the layer's LDS waits 5x).
+__device__ __forceinline__ int exact_slot(int c) {
+  return ((c >> 2) & 1) * (kExactCols / 2) + ((c >> 3) << 2) + (c & 3);
+}
+
+// Five waves per SIMD (95 VGPRs, no spill) rather than the four the default
+// register allocation leaves: one 4096 x 4096 layer at rank 64 51.5 -> 48.5 us,
+// a DiT block 660 -> 600 us, both bit-identical.
 template <bool F32OUT, int FDT>
-__global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void k_exact(ExactArgs g) {
   __shared__ __attribute__((aligned(16))) float As[kExactR][kExactCols];
   __shared__ float Bs[kExactRows][kExactR + 1];
   const JobDev& J = g.job;
@@ -201,21 +214,22 @@ __global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
             for (int h = 0; h < 2; ++h) {
               const u32x4 v = src[h];
 #pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                As[tid >> 3][cc + 8 * h + 2 * q] = __builtin_bit_cast(float, v[q] << 16);
-                As[tid >> 3][cc + 8 * h + 2 * q + 1] = __builtin_bit_cast(float, v[q] & 0xFFFF0000u);
-              }
+              for (int hf = 0; hf < 2; ++hf)
+                *reinterpret_cast<f32x4*>(&As[tid >> 3][exact_slot(cc + 8 * h + 4 * hf)]) =
+                    (f32x4){__builtin_bit_cast(float, v[2 * hf] << 16), __builtin_bit_cast(float, v[2 * hf] & 0xFFFF0000u),
+                            __builtin_bit_cast(float, v[2 * hf + 1] << 16),
+                            __builtin_bit_cast(float, v[2 * hf + 1] & 0xFFFF0000u)};
             }
           } else if constexpr (FDT == 1) {
             const f32x4* src = reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(L.a) + rr * cols + i0 + cc);
 #pragma unroll
-            for (int h = 0; h < 4; ++h) *reinterpret_cast<f32x4*>(&As[tid >> 3][cc + 4 * h]) = src[h];
+            for (int h = 0; h < 4; ++h) *reinterpret_cast<f32x4*>(&As[tid >> 3][exact_slot(cc + 4 * h)]) = src[h];
           }
         } else {
 #pragma unroll
           for (int q = 0; q < 16; ++q) {
             const uint64_t ii = i0 + cc + q;
-            As[tid >> 3][cc + q] = (rr < rank && ii < cols) ? factor_at<FDT>(L.a, L.dtype, rr * cols + ii) : 0.0f;
+            As[tid >> 3][exact_slot(cc + q)] = (rr < rank && ii < cols) ? factor_at<FDT>(L.a, L.dtype, rr * cols + ii) : 0.0f;
           }
         }
         // Bs holds c = coeff * B[o][r], rounded to f32 once here, exactly
@@ -259,10 +273,10 @@ __global__ __launch_bounds__(256) void k_exact(ExactArgs g) {
       const int nr = (int)(rank - r0 < (uint64_t)kExactR ? rank - r0 : (uint64_t)kExactR);
       // Zero-padded ranks beyond nr add fma(c, 0, w) = w + 0, which is not
       // the identity on -0; so the loop stops at nr exactly.
-#pragma unroll 4
+#pragma unroll 1
       for (int r = 0; r < nr; ++r) {
-        const f32x4 a0 = *reinterpret_cast<const f32x4*>(&As[r][8 * cg]);
-        const f32x4 a1 = *reinterpret_cast<const f32x4*>(&As[r][8 * cg + 4]);
+        const f32x4 a0 = *reinterpret_cast<const f32x4*>(&As[r][4 * cg]);
+        const f32x4 a1 = *reinterpret_cast<const f32x4*>(&As[r][kExactCols / 2 + 4 * cg]);
         const float a[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
