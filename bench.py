@@ -694,8 +694,8 @@ def main():
     ceiling = stream_ceiling(ctx, hip, stream, lead) if default_run else None
     if ceiling:
         log(f"streaming dequant ceiling {ceiling['GBps']:.0f} GB/s")
-        lead.calibration_copies(hip, stream)
-        ctx.synchronize()
+    lead.calibration_copies(hip, stream)
+    ctx.synchronize()
     lead.free()
     ctx.close()
 
