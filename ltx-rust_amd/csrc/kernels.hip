@@ -305,10 +305,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void k
         u32x4 v;
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = pack_bf16(acc[k][2 * q], acc[k][2 * q + 1]);
-        uint64_t any = 0;
+        float t[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) any |= __builtin_amdgcn_ballot_w64(__builtin_isnan(acc[k][j]));
-        if (any) {
+        for (int j = 0; j < 8; ++j) t[j & 3] = nan_probe(t[j & 3], acc[k][j]);
+        if (any_nan_wave(t[0], t[1], t[2], t[3])) {
 #pragma unroll
           for (int q = 0; q < 4; ++q)
             v[q] = (uint32_t)bf16_rne(acc[k][2 * q]) | ((uint32_t)bf16_rne(acc[k][2 * q + 1]) << 16);
@@ -359,7 +359,7 @@ __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i
     Acc<KS> acc;
     pp_mfma<KS, BSW>(J, fa, AT, LD, tid, acc);
     if constexpr (WFIRST || KS == 1) pp_issue_f<KS, FULL, BSW>(J, i0, hasB ? gB : gA, tid, fb);
-    pp_epilogue<F32OUT, KS, FULL, FMT>(J, fa, acc, i0, gA, tid);
+    pp_epilogue<F32OUT, KS, FULL, FMT, !WFIRST>(J, fa, acc, i0, gA, tid);
   }
   // Re-read the A^T fragments for the second unit rather than keeping them
   // live (64 VGPRs) across the first unit's epilogue.
@@ -367,7 +367,7 @@ __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i
   if (hasB) {
     Acc<KS> acc;
     pp_mfma<KS, BSW>(J, fb, AT, LD, tid, acc);
-    pp_epilogue<F32OUT, KS, FULL, FMT>(J, fb, acc, i0, gB, tid);
+    pp_epilogue<F32OUT, KS, FULL, FMT, !WFIRST>(J, fb, acc, i0, gB, tid);
   }
 }
 

@@ -30,15 +30,26 @@ __device__ __forceinline__ float canon_nan(float x) {
   return __builtin_isnan(x) ? __builtin_bit_cast(float, kCanonNaN) : x;
 }
 
-// Canonicalise the NaNs among n values, paying only a compare per value when
-// the whole wave holds none (the usual case): the per-value NaN tests are
-// combined into one wave-wide mask, and the selects run only if it is set.
+// Accumulates x * 0 into t: t becomes NaN once any x is NaN (or infinite,
+// whose product with 0 is NaN too; for those the canonicalisation below is a
+// no-op, so the false alarm costs only time).
+__device__ __forceinline__ float nan_probe(float t, float x) { return __builtin_fmaf(x, 0.0f, t); }
+
+// True when any lane's probe accumulators hold a NaN: one wave-wide compare.
+// (A ballot per value kept one 64-bit mask per value live in SGPRs; the fused
+// epilogue's 64 of them spilled some 350 SGPRs into VGPR lanes.)
+__device__ __forceinline__ bool any_nan_wave(float t0, float t1, float t2, float t3) {
+  return __builtin_amdgcn_ballot_w64(__builtin_isnan((t0 + t1) + (t2 + t3))) != 0;
+}
+
+// Canonicalise the NaNs among n values, paying only an FMA per value when the
+// whole wave holds none (the usual case); the selects run only if it does.
 template <int N>
 __device__ __forceinline__ void canon_nan_wave(float* v) {
-  uint64_t any = 0;
+  float t[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int j = 0; j < N; ++j) any |= __builtin_amdgcn_ballot_w64(__builtin_isnan(v[j]));
-  if (any) {
+  for (int j = 0; j < N; ++j) t[j & 3] = nan_probe(t[j & 3], v[j]);
+  if (any_nan_wave(t[0], t[1], t[2], t[3])) {
 #pragma unroll
     for (int j = 0; j < N; ++j) v[j] = canon_nan(v[j]);
   }
@@ -511,7 +522,15 @@ __device__ __forceinline__ void pp_mfma(const PJ& J, const Frag<KS>& f, const ui
   }
 }
 
-template <bool F32OUT, int KS, bool FULL, int FMT, class FragT>
+// PROBE: the epilogue's NaN test as FMA probes and one wave-wide compare
+// (launches of more than one round of workgroups: DiT block 152.7 -> 150.3 us,
+// mixed block 266 -> 260 us, against one 64-bit ballot mask per value, which
+// the compiler kept live in SGPRs and spilled to VGPR lanes). One-round
+// launches keep the per-value ballots: with the probe one 4096 x 4096 layer
+// took 12.9 us instead of 11.7 (alternating runs, one box; the compiler lays
+// that schedule's epilogue and second unit out differently, and which part of
+// the new layout costs the time was not isolated).
+template <bool F32OUT, int KS, bool FULL, int FMT, bool PROBE, class FragT>
 __device__ __forceinline__ void pp_epilogue(const PJ& J, const FragT& f, Acc<KS>& a, uint32_t i0, uint32_t g0,
                                             int tid) {
   const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
@@ -538,13 +557,26 @@ __device__ __forceinline__ void pp_epilogue(const PJ& J, const FragT& f, Acc<KS>
   // FP8 NaN codes decode to the reference's one NaN (f32::NAN); 16-bit bases
   // keep what the arithmetic makes of theirs.
   if constexpr (FMT <= 1) {
-    uint64_t any = 0;
+    bool any;
+    if constexpr (PROBE) {
+      float t[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+      for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb)
+        for (int nb = 0; nb < 8; ++nb)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) any |= __builtin_amdgcn_ballot_w64(__builtin_isnan(a.v[mb][nb][v]));
+          for (int v = 0; v < 4; ++v) t[v] = nan_probe(t[v], a.v[mb][nb][v]);
+      any = any_nan_wave(t[0], t[1], t[2], t[3]);
+    } else {
+      uint64_t m = 0;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) m |= __builtin_amdgcn_ballot_w64(__builtin_isnan(a.v[mb][nb][v]));
+      any = m != 0;
+    }
     if (any) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
@@ -578,12 +610,6 @@ __device__ __forceinline__ void pp_epilogue(const PJ& J, const FragT& f, Acc<KS>
   }
 }
 
-template <bool F32OUT, int KS, int FMT>
-__device__ __forceinline__ void pp_epilogue_any(const PJ& J, const Frag<KS>& f, Acc<KS>& a, uint32_t i0,
-                                                uint32_t g0, int tid) {
-  if (g0 + 128 <= J.rows && i0 + 128 <= J.cols) pp_epilogue<F32OUT, KS, true, FMT>(J, f, a, i0, g0, tid);
-  else pp_epilogue<F32OUT, KS, false, FMT>(J, f, a, i0, g0, tid);
-}
 
 }  // namespace
 }  // namespace ltxw

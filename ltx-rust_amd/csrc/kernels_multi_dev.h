@@ -316,13 +316,13 @@ __device__ __forceinline__ void pair_units_multi(const PJM<KS>& M, uint16_t* AT,
     Acc<KS> acc;
     pm_mfma<KS, FDT, B16, BSW>(M, fa, AT, LD, tid, acc);
     pm_issue_f<KS, FULL, FDT, B16, BSW>(M, hasB ? gB : gA, tid, fb);
-    pp_epilogue<F32OUT, KS, FULL, FMT>(M.base, fa, acc, i0, gA, tid);
+    pp_epilogue<F32OUT, KS, FULL, FMT, !WFIRST>(M.base, fa, acc, i0, gA, tid);
   }
   asm volatile("" ::: "memory");
   if (hasB) {
     Acc<KS> acc;
     pm_mfma<KS, FDT, B16, BSW>(M, fb, AT, LD, tid, acc);
-    pp_epilogue<F32OUT, KS, FULL, FMT>(M.base, fb, acc, i0, gB, tid);
+    pp_epilogue<F32OUT, KS, FULL, FMT, !WFIRST>(M.base, fb, acc, i0, gB, tid);
   }
 }
 
