@@ -11,9 +11,11 @@ r32 + r128, 4096x4104 and 4104x16384 edge tensors), the streaming-dequant
 ceiling of the same 1 B in / 2 B out pattern, and whole-model
 materialisation from safetensors files (--e2e). Kernel inputs are resident
 in HBM before timing; consecutive steps rotate over >= 1 GiB of distinct
-buffers so the 256 MB MALL cannot serve repeats; large dequant launches are
-queued ahead of the timed steps so that those run back to back on the GPU
-whatever the host's submission rate (also under a profiler).
+buffers so the 256 MB MALL cannot serve repeats; after the warmup and a
+synchronize, 200 ms of large dequant launches (--lead-ms) run ahead of the
+timed steps, so that those start with the GPU in its loaded steady state and
+run back to back on the GPU whatever the host's submission rate (also under a
+profiler).
 
 value     = algorithmic bytes per step * steps / timed seconds (GB/s), with
             algorithmic bytes = out*in (FP8) + 2*out*in (bf16 out) + scale
@@ -477,13 +479,18 @@ def main_model(args):
 
 class Lead:
     """Large streaming-dequant launches queued on the compute stream just
-    before a timed region, so that the timed launches queue up behind them
-    and run back to back even when the host submits them slower than the GPU
-    runs them (a profiler's per-launch cost). 2^30 FP8 elements of random
-    non-NaN codes per launch (a 64 MiB random block repeated; about 0.55 ms
-    per launch, so few launches cover a long submission); not part of any
-    timed figure except the streaming ceiling, which times these launches
-    themselves."""
+    before each timed region (--lead-ms, 200 ms by default): the GPU runs
+    them between the pre-timing synchronize and the first timed launch, so
+    the timed launches start with the GPU in its loaded steady state (clocks
+    and power management settle over tens of milliseconds of load) and,
+    under a profiler whose per-launch host cost exceeds the kernels' time,
+    still run back to back. 2^30 FP8 elements of random non-NaN codes per
+    launch (a 64 MiB random block repeated; about 0.55 ms each). Not part of
+    any timed figure except the streaming ceiling, which times these
+    launches themselves. Measured on one box (us per step): one layer over
+    200 steps 11.54-11.57 behind 200 ms of lead, 11.75 behind 10 ms, against
+    11.50-11.52 over 2000 steps; the mixed block 257.7-257.9 behind 200 ms,
+    258.2-258.7 over 800 steps without a lead, 264 over 200 steps without."""
 
     N = 1 << 30
     LAUNCH_US = 550.0
@@ -524,12 +531,12 @@ class Lead:
             self.ctx.free(p)
 
 
-def stream_ceiling(ctx, hip, stream, lead, reps=20):
+def stream_ceiling(ctx, hip, stream, lead, reps=20, lead_us=0.0):
     """The library's streaming dequant (16 FP8 bytes in, 32 bytes of bf16 out
     per thread) over 2^30 elements: the 1 B in / 2 B out pattern with no tile
     structure, the ceiling the fused kernels' traffic is compared with. `reps`
     launches timed back to back behind a queued lead."""
-    lead.queue(reps * 20.0)
+    lead.queue(max(reps * 20.0, lead_us))
     e0, e1 = hip.event(), hip.event()
     hip.record(e0, stream)
     lead.launch(reps)
@@ -540,7 +547,7 @@ def stream_ceiling(ctx, hip, stream, lead, reps=20):
             "us": round(us, 2), "GBps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4), "launches": reps}
 
 
-def kernel_config(name, ctx, hip, stream, lead, steps, warmup, exact=False, check_rows=64):
+def kernel_config(name, ctx, hip, stream, lead, steps, warmup, exact=False, check_rows=64, lead_us=0.0):
     """Times `steps` launches of one workload (after `warmup`), checks the
     last instance written against the oracle on sampled rows, and returns
     the figures of that workload."""
@@ -563,8 +570,9 @@ def kernel_config(name, ctx, hip, stream, lead, steps, warmup, exact=False, chec
         for k in range(warmup):
             ctx.grouped(descs[k % n_inst])
         ctx.synchronize()
-        # Queue ahead of the timed launches (see Lead), then time them.
-        lead.queue(steps * 50.0)
+        # Pre-heat (see Lead), then the timed launches queue up behind it.
+        if lead_us > 0:
+            lead.queue(lead_us)
         t_start, t_end = hip.event(), hip.event()
         hip.record(t_start, stream)
         h0 = time.perf_counter()
@@ -615,7 +623,8 @@ def kernel_config(name, ctx, hip, stream, lead, steps, warmup, exact=False, chec
                 "us": round(us, 3), "GBps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4),
                 "algorithmic_bytes": step_bytes, "lora_flops": flops,
                 "traffic": traffic, "traffic_over_algorithmic": round(traffic / step_bytes, 4) if traffic else None,
-                "host_submit_us_per_step": round(host_s / steps * 1e6, 2), "parity": par, "_cases": cases}
+                "host_submit_us_per_step": round(host_s / steps * 1e6, 2), "lead_us": round(lead_us),
+                "parity": par, "_cases": cases}
     finally:
         for p in allocs:
             ctx.free(p)
@@ -629,6 +638,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--lead-ms", type=float, default=200.0,
+                    help="ms of streaming-dequant launches queued ahead of each timed region (the GPU's loaded steady "
+                         "state at the first timed launch; back-to-back launches under a profiler); 0 for none")
     ap.add_argument("--workload", default="layer", choices=sorted(WORKLOAD_TEXT))
     ap.add_argument("--configs", default="auto",
                     help="comma-separated kernel workloads measured beside the headline one "
@@ -681,17 +693,18 @@ def main():
     ctx = lw.Context(0)
     stream = ctx.stream()
     lead = Lead(ctx)
-    head = kernel_config(args.workload, ctx, hip, stream, lead, args.steps, args.warmup, exact=args.exact)
+    head = kernel_config(args.workload, ctx, hip, stream, lead, args.steps, args.warmup, exact=args.exact,
+                         lead_us=args.lead_ms * 1e3)
     cases = head.pop("_cases")
     value = head["GBps"]
     configs = {CONFIG_OF.get(args.workload, args.workload): dict(head, name=args.workload)}
     csteps = args.config_steps or max(args.steps, 20)
     config_cases = {}
     for name in extra:
-        r = kernel_config(name, ctx, hip, stream, lead, csteps, min(args.warmup, 5) or 1)
+        r = kernel_config(name, ctx, hip, stream, lead, csteps, min(args.warmup, 5) or 1, lead_us=args.lead_ms * 1e3)
         config_cases[name] = r.pop("_cases")
         configs[CONFIG_OF.get(name, name)] = dict(r, name=name)
-    ceiling = stream_ceiling(ctx, hip, stream, lead) if default_run else None
+    ceiling = stream_ceiling(ctx, hip, stream, lead, lead_us=args.lead_ms * 1e3) if default_run else None
     if ceiling:
         log(f"streaming dequant ceiling {ceiling['GBps']:.0f} GB/s")
     lead.calibration_copies(hip, stream)
