@@ -340,6 +340,12 @@ template <bool F32OUT, int KS, int FMT, bool FULL, bool BSW, bool WFIRST>
 __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i0, uint32_t gA, uint32_t gB,
                                            bool hasB, int tid) {
   constexpr int LD = 32 * KS + 8;
+  // Raised wave priority while this wave issues its loads: where a wave of
+  // another workgroup is in its epilogue on the same SIMD, the loads go out
+  // first, so more memory requests are in flight (DiT block 149.2 ->
+  // 146.9 us, one layer 11.53 -> 11.42 us, alternating runs on one box; the
+  // several-LoRA kernel measured slower with it, mixed block 261 -> 265.5 us).
+  __builtin_amdgcn_s_setprio(2);
   Stage<KS> st;
   Frag<KS> fa, fb;
   if constexpr (WFIRST) {
@@ -353,6 +359,7 @@ __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i
     pp_issue_w<KS, FULL>(J, i0, gA, tid, fa);
   }
   pp_issue_w<KS, FULL>(J, i0, hasB ? gB : gA, tid, fb);
+  __builtin_amdgcn_s_setprio(0);
   pp_stage<KS>(st, AT, LD, tid);
   __syncthreads();
   {
