@@ -340,15 +340,16 @@ template <bool F32OUT, int KS, int FMT, bool FULL, bool BSW, bool WFIRST>
 __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i0, uint32_t gA, uint32_t gB,
                                            bool hasB, int tid) {
   constexpr int LD = 32 * KS + 8;
-  // Raised wave priority while this wave issues its loads: where a wave of
-  // another workgroup is in its epilogue on the same SIMD, the loads go out
-  // first, so more memory requests are in flight (DiT block 149.2 ->
-  // 146.9 us, one layer 11.53 -> 11.42 us, alternating runs on one box; the
-  // several-LoRA kernel measured slower with it, mixed block 261 -> 265.5 us).
-  __builtin_amdgcn_s_setprio(2);
   Stage<KS> st;
   Frag<KS> fa, fb;
+  // Raised wave priority from the first FP8 load to the last load of the
+  // issue phase: where a wave of another workgroup is in its epilogue on the
+  // same SIMD, these loads go out first, so more memory requests are in
+  // flight. Alternating runs on one box: DiT block 149.2 -> 146.9 us with
+  // the priority over the whole issue phase, 147.1 -> 146.2 us more with it
+  // from the first FP8 load on; one layer (FP8 first) 11.58 -> 11.44 us.
   if constexpr (WFIRST) {
+    __builtin_amdgcn_s_setprio(2);
     pp_issue_w<KS, FULL>(J, i0, gA, tid, fa);
     pp_issue_a<KS>(J, i0, tid, st);
     pp_issue_f<KS, FULL, BSW>(J, i0, gA, tid, fa);
@@ -356,6 +357,7 @@ __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i
     pp_issue_a<KS>(J, i0, tid, st);
     pp_issue_f<KS, FULL, BSW>(J, i0, gA, tid, fa);
     if constexpr (KS >= 2) pp_issue_f<KS, FULL, BSW>(J, i0, hasB ? gB : gA, tid, fb);
+    __builtin_amdgcn_s_setprio(2);
     pp_issue_w<KS, FULL>(J, i0, gA, tid, fa);
   }
   pp_issue_w<KS, FULL>(J, i0, hasB ? gB : gA, tid, fb);
