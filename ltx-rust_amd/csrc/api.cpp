@@ -254,14 +254,11 @@ int run_exact(ltxw_ctx* ctx, const ltxw_tensor_desc& d, const ltxw::DescEx* ex) 
 
 // Dequant without LoRA: vector kernel on 16-element chunks, generic on the rest.
 int run_dequant(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t n) {
-  // Tensors up to an FFN matrix: the tiled kernel (every unit's bytes of a
-  // workgroup requested up front).
+  // Tensors up to an FFN matrix: the tiled kernel.
   if (n <= ltxw::kTileMaxElems && d.cols % 8 == 0 && aligned(d.w, 16) && aligned(d.out, 16) &&
       (d.scale_mode != LTXW_SCALE_ROW || aligned(d.scales, 16))) {
     const uint32_t bands = (uint32_t)((d.cols + ltxw::kBandCols - 1) / ltxw::kBandCols);
-    const int64_t work_units = (int64_t)bands * ((d.rows + ltxw::kUnitRows - 1) / ltxw::kUnitRows);
-    ltxw::DequantTileArgs a{d.w, d.out, d.scales, (uint32_t)d.rows, (uint32_t)d.cols, bands,
-                            (uint32_t)ltxw::choose_units(work_units, ctx->cu_count)};
+    ltxw::DequantTileArgs a{d.w, d.out, d.scales, (uint32_t)d.rows, (uint32_t)d.cols, bands};
     HIP_TRY(ctx, ltxw::launch_dequant_tile(a, d.fmt, d.scale_mode, d.out_dtype == LTXW_OUT_F32, ctx->compute),
             "tiled dequant kernel launch");
     return LTXW_OK;
@@ -278,11 +275,6 @@ int run_dequant(ltxw_ctx* ctx, const ltxw_tensor_desc& d, uint64_t n) {
 }
 
 }  // namespace
-
-int ltxw::choose_units(int64_t units, int cu_count) {
-  const int64_t cus = cu_count > 0 ? cu_count : 256;
-  return units <= 8 * cus ? 4 : 2;
-}
 
 namespace {
 

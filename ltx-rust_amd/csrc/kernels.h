@@ -146,17 +146,15 @@ hipError_t launch_dequant(const DequantArgs& a, int fmt, int scale_mode, bool f3
                           hipStream_t stream);
 
 // Tiled dequant for tensors of up to kTileMaxElems elements (an FFN matrix
-// of the DiT has 2^26): the fused kernels' access pattern (`units`
-// 128-row x 128-column units per workgroup, 8 FP8 bytes per lane and row)
-// without the LoRA. Requirements
-// checked by the caller: cols % 8 == 0; w, out (and row scales) 16-byte
-// aligned; rows * cols * 4 < 2^32.
+// of the DiT has 2^26): the fused kernels' access pattern (one 128-row x
+// 128-column unit per workgroup, 8 FP8 bytes per lane and row) without the
+// LoRA. Requirements checked by the caller: cols % 8 == 0; w, out (and row
+// scales) 16-byte aligned; rows * cols * 4 < 2^32.
 struct DequantTileArgs {
   const uint8_t* w;
   void* out;
   const float* scales;
   uint32_t rows, cols, bands_n;
-  uint32_t units;  // 128-row units per workgroup: 1, 2 or 4
 };
 constexpr uint64_t kTileMaxElems = 1ull << 27;
 hipError_t launch_dequant_tile(const DequantTileArgs& a, int fmt, int scale_mode, bool f32out,
@@ -190,14 +188,9 @@ hipError_t launch_fused_multi_base16(const JobTable& t, bool f32out, int ks, hip
 // workgroup of the fused kernels takes a pair of vertically adjacent units
 // of one band (kPairRows rows): on one 4096 x 4096 layer with a rank-64
 // LoRA, 4 units per workgroup measured no faster than 2. The tiled dequant
-// kernel takes DequantTileArgs::units of them.
+// kernel takes one unit per workgroup.
 constexpr int kUnitRows = kWavesPerGroup * kStripRows;
 constexpr int kPairRows = 2 * kUnitRows;
-// Units per workgroup of the tiled dequant kernel for a launch of `units`
-// work units in all: 4 while that makes at most two workgroups per CU
-// (fewer, longer workgroups cut the launch's ramp and drain), 2 above. Measured (4096 x 4096): 4 units
-// 9.15 us, 2 units 9.98, 1 unit 10.66.
-int choose_units(int64_t units, int cu_count);
 
 // Padded K extent of one LoRA in the fused kernel's LDS stage.
 __host__ __device__ inline int pad_rank(int rank) { return (rank + 31) / 32 * 32; }

@@ -406,13 +406,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS == 1 || 
 
 // ---------------------------------------------------------------------------
 // (a') Tiled dequant: the fused kernels' tile walk and lane layout without
-// the LoRA. A workgroup takes U (1, 2 or 4) vertically adjacent 128 x 128
-// units of a column band; lane l of wave w handles, in each unit, the 8
-// columns i0 + 8 (l % 16) .. +7 of rows r0 + 4 (l / 16) + {0..3, 16..19}
-// with r0 = g0 + 32 w. Every unit's bytes are requested before the first
-// unit is converted. Faster than the streaming kernel up to an FFN matrix
-// (4096 x 4096: 9.2 against 11.5 us; 16384 x 4096: 37.8 against 38.7 us with
-// the streaming kernel at its best setting).
+// the LoRA. A workgroup takes one 128 x 128 unit of a column band; lane l of
+// wave w handles the 8 columns i0 + 8 (l % 16) .. +7 of rows
+// r0 + 4 (l / 16) + {0..3, 16..19} with r0 = g0 + 32 w. The wave requests its
+// FP8 bytes at raised priority (s_setprio 2), so that where four workgroups
+// share a CU a wave's loads go out ahead of other waves' conversions and
+// stores. Alternating runs on one box, 200 launches behind the bench's
+// pre-heat: 4096 x 4096 9.65 -> 8.9 us (5.65 TB/s), 16384 x 4096 and
+// 4096 x 16384 37.0 -> 34.1-34.9 us, 8192 x 8192 38.2 -> 35.0 us; two units
+// per workgroup (every unit's bytes first) with the priority 9.1 / 36.4-37.1 /
+// 37.3 us, four units 9.8 us; without the priority four units were the
+// fastest form (9.65 us; one unit 10.7).
 // ---------------------------------------------------------------------------
 template <int SMODE, bool FULL>
 __device__ __forceinline__ void dqt_load(const DequantTileArgs& a, uint32_t i0, uint32_t g0, int tid, u32x2 (&wv)[8],
@@ -482,48 +486,35 @@ __device__ __forceinline__ void dqt_store(const DequantTileArgs& a, uint32_t i0,
   }
 }
 
-// U units of a band: every unit's bytes are requested before the first unit
-// is converted.
-template <int FMT, int SMODE, bool F32OUT, bool FULL, int U>
-__device__ __forceinline__ void dqt_units(const DequantTileArgs& a, uint32_t i0, uint32_t g0, int tid, float tscale) {
-  u32x2 w[U][8];
-  float sc[U][8];
-#pragma unroll
-  for (int u = 0; u < U; ++u) dqt_load<SMODE, FULL>(a, i0, g0 + kUnitRows * u, tid, w[u], sc[u], tscale);
-#pragma unroll
-  for (int u = 0; u < U; ++u)
-    if (FULL || g0 + kUnitRows * u < a.rows) dqt_store<FMT, SMODE, F32OUT, FULL>(a, i0, g0 + kUnitRows * u, tid, w[u], sc[u]);
+template <int FMT, int SMODE, bool F32OUT, bool FULL>
+__device__ __forceinline__ void dqt_unit(const DequantTileArgs& a, uint32_t i0, uint32_t g0, int tid, float tscale) {
+  u32x2 w[8];
+  float sc[8];
+  __builtin_amdgcn_s_setprio(2);
+  dqt_load<SMODE, FULL>(a, i0, g0, tid, w, sc, tscale);
+  __builtin_amdgcn_s_setprio(0);
+  dqt_store<FMT, SMODE, F32OUT, FULL>(a, i0, g0, tid, w, sc);
 }
 
-template <int FMT, int SMODE, bool F32OUT, int U>
+template <int FMT, int SMODE, bool F32OUT>
 __global__ __launch_bounds__(256) void k_dequant_tile(DequantTileArgs a) {
   const int tid = threadIdx.x;
   const uint32_t p = blockIdx.x;
   const uint32_t i0 = (p % a.bands_n) * kBandCols;
-  const uint32_t g0 = (p / a.bands_n) * (U * kUnitRows);
-  const bool full = g0 + U * kUnitRows <= a.rows && i0 + kBandCols <= a.cols;
+  const uint32_t g0 = (p / a.bands_n) * kUnitRows;
+  const bool full = g0 + kUnitRows <= a.rows && i0 + kBandCols <= a.cols;
   const float tscale = SMODE == 1 ? *G(uni_ptr(a.scales)) : 1.0f;
-  if (full) dqt_units<FMT, SMODE, F32OUT, true, U>(a, i0, g0, tid, tscale);
-  else dqt_units<FMT, SMODE, F32OUT, false, U>(a, i0, g0, tid, tscale);
-}
-
-template <int FMT, int SMODE, int U>
-hipError_t dequant_tile_u(const DequantTileArgs& a, bool f32out, dim3 grid, hipStream_t s) {
-  if (f32out)
-    hipLaunchKernelGGL((k_dequant_tile<FMT, SMODE, true, U>), grid, dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL((k_dequant_tile<FMT, SMODE, false, U>), grid, dim3(256), 0, s, a);
-  return hipGetLastError();
+  if (full) dqt_unit<FMT, SMODE, F32OUT, true>(a, i0, g0, tid, tscale);
+  else dqt_unit<FMT, SMODE, F32OUT, false>(a, i0, g0, tid, tscale);
 }
 
 template <int FMT, int SMODE>
 hipError_t dequant_tile_out(const DequantTileArgs& a, bool f32out, dim3 grid, hipStream_t s) {
-  switch (a.units) {
-    case 1: return dequant_tile_u<FMT, SMODE, 1>(a, f32out, grid, s);
-    case 2: return dequant_tile_u<FMT, SMODE, 2>(a, f32out, grid, s);
-    case 4: return dequant_tile_u<FMT, SMODE, 4>(a, f32out, grid, s);
-    default: return hipErrorInvalidValue;
-  }
+  if (f32out)
+    hipLaunchKernelGGL((k_dequant_tile<FMT, SMODE, true>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((k_dequant_tile<FMT, SMODE, false>), grid, dim3(256), 0, s, a);
+  return hipGetLastError();
 }
 
 template <int FMT>
@@ -566,9 +557,7 @@ hipError_t launch_dequant(const DequantArgs& a, int fmt, int scale_mode, bool f3
 
 hipError_t launch_dequant_tile(const DequantTileArgs& a, int fmt, int scale_mode, bool f32out,
                                hipStream_t stream) {
-  if (a.units != 1 && a.units != 2 && a.units != 4) return hipErrorInvalidValue;
-  const uint64_t rows_per = (uint64_t)a.units * kUnitRows;
-  const uint64_t groups = (uint64_t)a.bands_n * ((a.rows + rows_per - 1) / rows_per);
+  const uint64_t groups = (uint64_t)a.bands_n * ((a.rows + kUnitRows - 1) / kUnitRows);
   if (groups == 0) return hipSuccess;
   dim3 grid((unsigned)groups);
   return fmt == 0 ? dequant_tile_scale<0>(a, scale_mode, f32out, grid, stream)
