@@ -514,9 +514,10 @@ class Lead:
         for _ in range(n):
             self.ctx.dequant(self.w, self.N >> 14, 1 << 14, self.lw.FMT_E4M3FN, self.lw.SCALE_TENSOR, self.s, self.out)
 
-    def queue(self, host_us):
-        """Enough launches to cover host_us of host-side submission."""
-        self.launch(int(host_us / self.LAUNCH_US) + 1)
+    def queue(self, us):
+        """Launches that keep the GPU busy for about `us` microseconds
+        (LAUNCH_US each)."""
+        self.launch(int(us / self.LAUNCH_US) + 1)
 
     def calibration_copies(self, hip, stream, n=4):
         """n device-to-device copies of 256 MiB (the first half of the output
