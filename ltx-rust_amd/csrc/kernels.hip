@@ -342,17 +342,20 @@ __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i
   constexpr int LD = 32 * KS + 8;
   Stage<KS> st;
   Frag<KS> fa, fb;
-  // Raised wave priority from the first FP8 load to the last load of the
-  // issue phase: where a wave of another workgroup is in its epilogue on the
-  // same SIMD, these loads go out first, so more memory requests are in
-  // flight. Alternating runs on one box: DiT block 149.2 -> 146.9 us with
-  // the priority over the whole issue phase, 147.1 -> 146.2 us more with it
-  // from the first FP8 load on; one layer (FP8 first) 11.58 -> 11.44 us.
+  // Raised wave priority while the FP8 bytes are requested: where a wave of
+  // another workgroup is in its epilogue on the same SIMD, these loads go
+  // out first, so more memory requests are in flight. Alternating runs on
+  // one box: DiT block 149.2 -> 146.9 us with the priority over the whole
+  // issue phase, 147.1 -> 146.2 us more with it on the FP8 loads only; one
+  // layer (FP8 first) 11.58 -> 11.48 us over the whole issue phase,
+  // 11.49 -> 11.37 us more on the FP8 loads only.
   if constexpr (WFIRST) {
     __builtin_amdgcn_s_setprio(2);
     pp_issue_w<KS, FULL>(J, i0, gA, tid, fa);
+    __builtin_amdgcn_s_setprio(0);
     pp_issue_a<KS>(J, i0, tid, st);
     pp_issue_f<KS, FULL, BSW>(J, i0, gA, tid, fa);
+    __builtin_amdgcn_s_setprio(2);
   } else {
     pp_issue_a<KS>(J, i0, tid, st);
     pp_issue_f<KS, FULL, BSW>(J, i0, gA, tid, fa);
