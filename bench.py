@@ -487,7 +487,7 @@ class Lead:
     still run back to back. 2^30 FP8 elements of random non-NaN codes per
     launch (a 64 MiB random block repeated; about 0.55 ms each). Not part of
     any timed figure except the streaming ceiling, which times these
-    launches themselves. Measured on one box (us per step): one layer over
+    launches themselves. Measured on one machine (us per step): one layer over
     200 steps 11.54-11.57 behind 200 ms of lead, 11.75 behind 10 ms, against
     11.50-11.52 over 2000 steps; the mixed block 257.7-257.9 behind 200 ms,
     258.2-258.7 over 800 steps without a lead, 264 over 200 steps without."""

@@ -345,7 +345,7 @@ __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i
   // Raised wave priority while the FP8 bytes are requested: where a wave of
   // another workgroup is in its epilogue on the same SIMD, these loads go
   // out first, so more memory requests are in flight. Alternating runs on
-  // one box: DiT block 149.2 -> 146.9 us with the priority over the whole
+  // one machine: DiT block 149.2 -> 146.9 us with the priority over the whole
   // issue phase, 147.1 -> 146.2 us more with it on the FP8 loads only; one
   // layer (FP8 first) 11.58 -> 11.48 us over the whole issue phase,
   // 11.49 -> 11.37 us more on the FP8 loads only.
@@ -414,7 +414,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS == 1 || 
 // r0 + 4 (l / 16) + {0..3, 16..19} with r0 = g0 + 32 w. The wave requests its
 // FP8 bytes at raised priority (s_setprio 2), so that where four workgroups
 // share a CU a wave's loads go out ahead of other waves' conversions and
-// stores. Alternating runs on one box, 200 launches behind the bench's
+// stores. Alternating runs on one machine, 200 launches behind the bench's
 // pre-heat: 4096 x 4096 9.65 -> 8.9 us (5.65 TB/s), 16384 x 4096 and
 // 4096 x 16384 37.0 -> 34.1-34.9 us, 8192 x 8192 38.2 -> 35.0 us; two units
 // per workgroup (every unit's bytes first) with the priority 9.1 / 36.4-37.1 /

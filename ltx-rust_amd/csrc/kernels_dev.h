@@ -528,7 +528,7 @@ __device__ __forceinline__ void pp_mfma(const PJ& J, const Frag<KS>& f, const ui
 // the compiler kept live in SGPRs and spilled to VGPR lanes). One-round
 // launches keep the per-value ballots: with the probe one 4096 x 4096 layer
 // took 12.9 us instead of 11.7, and with an integer-max test (no SGPR spills
-// either) 13.2 us (alternating runs, one box; the compiler lays that
+// either) 13.2 us (alternating runs on one machine; the compiler lays that
 // schedule's epilogue and second unit out differently, and which part of the
 // new layout costs the time was not isolated).
 template <bool F32OUT, int KS, bool FULL, int FMT, bool PROBE, class FragT>

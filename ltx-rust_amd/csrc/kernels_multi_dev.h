@@ -308,7 +308,7 @@ __device__ __forceinline__ void pair_units_multi(const PJM<KS>& M, uint16_t* AT,
     pm_issue_a<KS, FDT>(M, i0, tid, st);
     pm_issue_f<KS, FULL, FDT, B16, BSW>(M, gA, tid, fa);
     // Raised wave priority while the FP8 bytes are requested, as in
-    // pair_units: mixed block 257 -> 254.5 us (alternating runs, one box;
+    // pair_units: mixed block 257 -> 254.5 us (alternating runs on one machine;
     // over the whole issue phase it measured slower, 261 -> 265.5 us). The
     // one-round schedule above was not measured with it and has none.
     __builtin_amdgcn_s_setprio(2);
