@@ -146,10 +146,11 @@ hipError_t launch_dequant(const DequantArgs& a, int fmt, int scale_mode, bool f3
                           hipStream_t stream);
 
 // Tiled dequant for tensors of up to kTileMaxElems elements (an FFN matrix
-// of the DiT has 2^26): the fused kernels' access pattern (one 128-row x
-// 128-column unit per workgroup, 8 FP8 bytes per lane and row) without the
-// LoRA. Requirements checked by the caller: cols % 8 == 0; w, out (and row
-// scales) 16-byte aligned; rows * cols * 4 < 2^32.
+// of the DiT has 2^26): the fused kernels' lane layout (8 FP8 bytes per lane
+// and row, 16 lanes per 128-column row segment) without the LoRA, kTileRows
+// rows x 128 columns per workgroup. Requirements checked by the caller:
+// cols % 8 == 0; w, out (and row scales) 16-byte aligned;
+// rows * cols * 4 < 2^32.
 struct DequantTileArgs {
   const uint8_t* w;
   void* out;
@@ -157,6 +158,7 @@ struct DequantTileArgs {
   uint32_t rows, cols, bands_n;
 };
 constexpr uint64_t kTileMaxElems = 1ull << 27;
+constexpr int kTileRows = 64;
 hipError_t launch_dequant_tile(const DequantTileArgs& a, int fmt, int scale_mode, bool f32out,
                                hipStream_t stream);
 
@@ -187,8 +189,8 @@ hipError_t launch_fused_multi_base16(const JobTable& t, bool f32out, int ks, hip
 // Rows of one work unit (a band of kBandCols columns by kUnitRows rows). A
 // workgroup of the fused kernels takes a pair of vertically adjacent units
 // of one band (kPairRows rows): on one 4096 x 4096 layer with a rank-64
-// LoRA, 4 units per workgroup measured no faster than 2. The tiled dequant
-// kernel takes one unit per workgroup.
+// LoRA, 4 units per workgroup measured no faster than 2. (The tiled dequant
+// kernel takes kTileRows rows per workgroup.)
 constexpr int kUnitRows = kWavesPerGroup * kStripRows;
 constexpr int kPairRows = 2 * kUnitRows;
 

@@ -408,63 +408,58 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS == 1 || 
 }
 
 // ---------------------------------------------------------------------------
-// (a') Tiled dequant: the fused kernels' tile walk and lane layout without
-// the LoRA. A workgroup takes one 128 x 128 unit of a column band; lane l of
-// wave w handles the 8 columns i0 + 8 (l % 16) .. +7 of rows
-// r0 + 4 (l / 16) + {0..3, 16..19} with r0 = g0 + 32 w. The wave requests its
-// FP8 bytes at raised priority (s_setprio 2), so that where four workgroups
-// share a CU a wave's loads go out ahead of other waves' conversions and
-// stores. Alternating runs on one machine, 200 launches behind the bench's
-// pre-heat: 4096 x 4096 9.65 -> 8.9 us (5.65 TB/s), 16384 x 4096 and
-// 4096 x 16384 37.0 -> 34.1-34.9 us, 8192 x 8192 38.2 -> 35.0 us; two units
-// per workgroup (every unit's bytes first) with the priority 9.1 / 36.4-37.1 /
-// 37.3 us, four units 9.8 us; without the priority four units were the
-// fastest form (9.65 us; one unit 10.7).
+// (a') Tiled dequant: the fused kernels' lane layout without the LoRA. A
+// workgroup takes 64 rows x 128 columns of a column band; lane l of wave w
+// handles the 8 columns i0 + 8 (l % 16) .. +7 of rows g0 + 16 w + 4 (l / 16)
+// + {0..3}. The wave requests its FP8 bytes at raised priority
+// (s_setprio 2), so that where several workgroups share a CU a wave's loads
+// go out ahead of other waves' conversions and stores. Alternating runs on
+// one machine, 200 launches behind the bench's pre-heat (4096 x 4096; FFN
+// 16384 x 4096 / 4096 x 16384; 8192 x 8192, us): 128-row tiles, four per
+// workgroup, no priority 9.65; 37.0 / 37.0; 38.2. 128-row tiles with the
+// priority, one per workgroup 8.9-9.0; 34.9-35.2 / 34.1-34.4; 35.0-35.2,
+// two 9.1, four 9.8. 64-row tiles with the priority 8.65-8.68; 35.1 /
+// 34.5-34.7; 34.8-34.9. 32-row tiles 10.1; 34.8 / 34.4; 34.7.
 // ---------------------------------------------------------------------------
 template <int SMODE, bool FULL>
-__device__ __forceinline__ void dqt_load(const DequantTileArgs& a, uint32_t i0, uint32_t g0, int tid, u32x2 (&wv)[8],
-                                         float (&sc)[8], float tscale) {
+__device__ __forceinline__ void dqt_load(const DequantTileArgs& a, uint32_t i0, uint32_t g0, int tid, u32x2 (&wv)[4],
+                                         float (&sc)[4], float tscale) {
   const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
-  const uint32_t rl = g0 + kStripRows * wave + 4 * lg;
+  const uint32_t rl = g0 + 16 * wave + 4 * lg;
   const uint32_t ecol = i0 + 8 * ln;
   const bool col_ok = FULL || ecol < a.cols;
   const uint32_t e0 = rl * a.cols + ecol;
 #pragma unroll
-  for (int g = 0; g < 8; ++g) {
-    const uint32_t dr = 16 * (g >> 2) + (g & 3);
+  for (int g = 0; g < 4; ++g) {
     wv[g] = (u32x2){0u, 0u};
-    if (col_ok && (FULL || rl + dr < a.rows)) wv[g] = ld_nt_at<u32x2>(a.w, e0 + dr * a.cols);
+    if (col_ok && (FULL || rl + g < a.rows)) wv[g] = ld_nt_at<u32x2>(a.w, e0 + g * a.cols);
   }
   if (SMODE == 2) {
+    if (FULL || rl + 3 < a.rows) {
+      const f32x4 q = ld_at<f32x4>(a.scales, 4 * rl);
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      const uint32_t rb = rl + 16 * mb;
-      if (FULL || rb + 3 < a.rows) {
-        const f32x4 q = ld_at<f32x4>(a.scales, 4 * rb);
+      for (int v = 0; v < 4; ++v) sc[v] = q[v];
+    } else {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) sc[4 * mb + v] = q[v];
-      } else {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) sc[4 * mb + v] = rb + v < a.rows ? ld_at<float>(a.scales, 4 * (rb + v)) : 1.0f;
-      }
+      for (int v = 0; v < 4; ++v) sc[v] = rl + v < a.rows ? ld_at<float>(a.scales, 4 * (rl + v)) : 1.0f;
     }
   } else {
 #pragma unroll
-    for (int g = 0; g < 8; ++g) sc[g] = tscale;
+    for (int g = 0; g < 4; ++g) sc[g] = tscale;
   }
 }
 
 template <int FMT, int SMODE, bool F32OUT, bool FULL>
 __device__ __forceinline__ void dqt_store(const DequantTileArgs& a, uint32_t i0, uint32_t g0, int tid,
-                                          const u32x2 (&wv)[8], const float (&sc)[8]) {
+                                          const u32x2 (&wv)[4], const float (&sc)[4]) {
   const int lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
-  const uint32_t rl = g0 + kStripRows * wave + 4 * lg;
+  const uint32_t rl = g0 + 16 * wave + 4 * lg;
   const uint32_t ecol = i0 + 8 * ln;
   const bool col_ok = FULL || ecol < a.cols;
   const uint32_t e0 = rl * a.cols + ecol;
-  float x[8][8];
+  float x[4][8];
 #pragma unroll
-  for (int g = 0; g < 8; ++g) {
+  for (int g = 0; g < 4; ++g) {
     decode4(wv[g][0], FMT, x[g]);
     decode4(wv[g][1], FMT, x[g] + 4);
     if (SMODE != 0) {
@@ -472,12 +467,11 @@ __device__ __forceinline__ void dqt_store(const DequantTileArgs& a, uint32_t i0,
       for (int j = 0; j < 8; ++j) x[g][j] = __builtin_fmaf(sc[g], x[g][j], 0.0f);
     }
   }
-  canon_nan_wave<64>(&x[0][0]);
+  canon_nan_wave<32>(&x[0][0]);
 #pragma unroll
-  for (int g = 0; g < 8; ++g) {
-    const uint32_t dr = 16 * (g >> 2) + (g & 3);
-    if (!(col_ok && (FULL || rl + dr < a.rows))) continue;
-    const uint32_t e = e0 + dr * a.cols;
+  for (int g = 0; g < 4; ++g) {
+    if (!(col_ok && (FULL || rl + g < a.rows))) continue;
+    const uint32_t e = e0 + g * a.cols;
     if (F32OUT) {
       st_nt_at<f32x4>(a.out, 4 * e, (f32x4){x[g][0], x[g][1], x[g][2], x[g][3]});
       st_nt_at<f32x4>(a.out, 4 * e + 16, (f32x4){x[g][4], x[g][5], x[g][6], x[g][7]});
@@ -491,8 +485,8 @@ __device__ __forceinline__ void dqt_store(const DequantTileArgs& a, uint32_t i0,
 
 template <int FMT, int SMODE, bool F32OUT, bool FULL>
 __device__ __forceinline__ void dqt_unit(const DequantTileArgs& a, uint32_t i0, uint32_t g0, int tid, float tscale) {
-  u32x2 w[8];
-  float sc[8];
+  u32x2 w[4];
+  float sc[4];
   __builtin_amdgcn_s_setprio(2);
   dqt_load<SMODE, FULL>(a, i0, g0, tid, w, sc, tscale);
   __builtin_amdgcn_s_setprio(0);
@@ -504,8 +498,8 @@ __global__ __launch_bounds__(256) void k_dequant_tile(DequantTileArgs a) {
   const int tid = threadIdx.x;
   const uint32_t p = blockIdx.x;
   const uint32_t i0 = (p % a.bands_n) * kBandCols;
-  const uint32_t g0 = (p / a.bands_n) * kUnitRows;
-  const bool full = g0 + kUnitRows <= a.rows && i0 + kBandCols <= a.cols;
+  const uint32_t g0 = (p / a.bands_n) * kTileRows;
+  const bool full = g0 + kTileRows <= a.rows && i0 + kBandCols <= a.cols;
   const float tscale = SMODE == 1 ? *G(uni_ptr(a.scales)) : 1.0f;
   if (full) dqt_unit<FMT, SMODE, F32OUT, true>(a, i0, g0, tid, tscale);
   else dqt_unit<FMT, SMODE, F32OUT, false>(a, i0, g0, tid, tscale);
@@ -560,7 +554,7 @@ hipError_t launch_dequant(const DequantArgs& a, int fmt, int scale_mode, bool f3
 
 hipError_t launch_dequant_tile(const DequantTileArgs& a, int fmt, int scale_mode, bool f32out,
                                hipStream_t stream) {
-  const uint64_t groups = (uint64_t)a.bands_n * ((a.rows + kUnitRows - 1) / kUnitRows);
+  const uint64_t groups = (uint64_t)a.bands_n * ((a.rows + kTileRows - 1) / kTileRows);
   if (groups == 0) return hipSuccess;
   dim3 grid((unsigned)groups);
   return fmt == 0 ? dequant_tile_scale<0>(a, scale_mode, f32out, grid, stream)
