@@ -77,6 +77,21 @@ def test_dequant_ragged_shapes_bit_exact(ctx, shape, scale_mode):
     assert np.array_equal(got, U.oracle_bf16(case))
 
 
+@pytest.mark.parametrize("shape", [(65, 4096), (200, 4104), (127, 136), (63, 8)])
+@pytest.mark.parametrize("fmt", [synth.E4M3FN, synth.E5M2])
+def test_dequant_partial_row_tiles_row_scales(ctx, shape, fmt):
+    """The tiled kernel takes 64 rows x 128 columns per workgroup: row counts
+    off a multiple of 64 (a last tile of 1, 8 or 63 rows) and a last band
+    of 8 columns, with one scale per row, in both output types."""
+    log("case: partial row tiles", shape, fmt)
+    case = synth.tensor_case(11, shape[0], shape[1], fmt, synth.SCALE_ROW, loras=())
+    for out_dtype in (lw.OUT_BF16, lw.OUT_F32):
+        got = run_case(ctx, case, out_dtype)
+        ref = U.oracle_bf16(case) if out_dtype == lw.OUT_BF16 else U.oracle_f32(case)
+        assert np.array_equal(got.view(np.uint16 if out_dtype == lw.OUT_BF16 else np.uint32),
+                              ref.view(np.uint16 if out_dtype == lw.OUT_BF16 else np.uint32)), out_dtype
+
+
 @pytest.mark.parametrize("w_offset,out_offset", [(1, 0), (0, 2), (3, 6), (8, 0)])
 def test_dequant_unaligned_pointers_bit_exact(ctx, w_offset, out_offset):
     log("case: unaligned", w_offset, out_offset)
