@@ -413,6 +413,36 @@ def test_grouped_calls_with_device_job_tables(ctx):
             d.free()
 
 
+@pytest.mark.parametrize("loras", [((64, 1.0),), ((32, 1.0), (32, -0.5))], ids=["r64", "r32+r32"])
+def test_grouped_call_inline_records_beyond_first_workgroup_array(ctx, loras):
+    """20 tensors of 2 K-steps in one grouped call: their records (20 x 128
+    bytes) still travel in the kernel arguments, but there are more of them
+    than the 16-entry array of first workgroups holds, so a workgroup finds
+    its record by a binary search over the inline records (the case of two
+    DiT blocks in one call). Every output equals the tensor's own
+    single-call result."""
+    log("case: 20 inline records", loras)
+    shapes = [(64 + 24 * k, 128 + 8 * (k % 7) * 8) for k in range(20)]
+    cases = [synth.tensor_case(5200 + k, r, c, synth.E4M3FN if k % 2 else synth.E5M2,
+                               synth.SCALE_ROW if k % 3 else synth.SCALE_TENSOR, loras=loras)
+             for k, (r, c) in enumerate(shapes)]
+    devs = [U.Dev(ctx, c) for c in cases]
+    try:
+        singles = []
+        for d in devs:
+            d.run()
+            singles.append(d.result())
+        for d in devs:
+            ctx.memset(d.out, 0xFF, d.n * d.ob)
+        ctx.grouped([{"w": d.w, "out": d.out, "scales": d.s, "rows": d.case["rows"], "cols": d.case["cols"],
+                      "fmt": d.case["fmt"], "scale_mode": d.case["scale_mode"], "loras": d.loras} for d in devs])
+        for k, (d, s) in enumerate(zip(devs, singles)):
+            assert np.array_equal(d.result(), s), "tensor %d" % k
+    finally:
+        for d in devs:
+            d.free()
+
+
 def test_grouped_block_matches_single_calls(ctx):
     """A grouped launch over mixed tensors equals per-tensor calls bit for bit."""
     log("case: grouped vs single")
