@@ -332,6 +332,7 @@ void write_records(const std::vector<ltxw::JobDev>& jobs, size_t first, size_t c
     h.qmask = j.qmask;
     h.cmul = j.cmul;
     h.coeff_out = j.coeff_out;
+    h.single = j.single;
     unsigned char* r = dst + k * record_bytes(ks);
     memcpy(r, &h, sizeof(h));
     memcpy(r + sizeof(h), j.step, (size_t)ks * sizeof(ltxw::StepDev));
@@ -345,31 +346,68 @@ int job_k(const ltxw::JobDev& j) {
   return k;
 }
 
+// Large launches: the last job's last rows (about kTailPairs pair
+// workgroups' worth, whole row pairs) become a job of single-unit workgroups
+// at the launch's end, so that the launch drains in narrow units: a DiT block
+// (8192 workgroups) 144.4-145.6 -> 141.7-142.2 us, with 256 pairs' worth
+// 143.1-144.0, with 1024 141.6-142.5 (alternating runs on one machine). Only
+// where the records stay in the kernel arguments.
+void split_tail(std::vector<ltxw::JobDev>& jobs, int64_t pairs, bool f32out, size_t rec) {
+  if (pairs <= (int64_t)ltxw::kRemapMinGrid || jobs.empty()) return;
+  if ((jobs.size() + 1) * rec > (size_t)ltxw::kInlineTableBytes || jobs.size() + 1 > (size_t)ltxw::kInlineBegins)
+    return;
+  ltxw::JobDev& L = jobs.back();
+  const int64_t row_pairs = (L.rows + ltxw::kPairRows - 1) / ltxw::kPairRows;
+  const int64_t take = std::min<int64_t>(row_pairs - 1, (ltxw::kTailPairs + L.bands_n - 1) / L.bands_n);
+  if (take <= 0) return;
+  const int64_t r1 = (row_pairs - take) * ltxw::kPairRows;
+  ltxw::JobDev T = L;
+  T.rows = L.rows - r1;
+  T.single = 1;
+  T.w = L.w + r1 * L.cols * ltxw::format_bytes(L.fmt);
+  T.out = (char*)L.out + r1 * L.cols * (f32out ? 4 : 2);
+  if (L.scale_mode == LTXW_SCALE_ROW) T.scales = L.scales + r1;
+  for (int l = 0; l < L.n_loras; ++l)
+    T.lora[l].b = (const uint16_t*)((const char*)L.lora[l].b +
+                                    r1 * (int64_t)L.lora[l].rank * factor_bytes(L.lora[l].dtype));
+  L.rows = r1;
+  jobs.push_back(T);
+}
+
 // One fused launch over `jobs` (all fused_ok, same out dtype, kernel, factor
 // type and K-steps): one workgroup per 128-column band and 256 rows of every
-// job.
+// job (128 rows in a split launch's single-unit job).
 int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool multi, int fdt, bool base16,
               bool noalloc) {
   if (jobs.empty()) return LTXW_OK;
   int kmax = 0;
   for (auto& j : jobs) kmax = std::max(kmax, job_k(j));
-  const int64_t group_rows = ltxw::kPairRows;
-  int64_t units = 0;  // workgroups (unit pairs)
-  for (auto& j : jobs) {
-    plan_fused(j);
-    j.unit_begin = units;
-    units += (int64_t)j.bands_n * ((j.rows + group_rows - 1) / group_rows);
-  }
-  if (units > INT32_MAX) return fail(ctx, LTXW_ERR_INVALID_ARG, "launch of %lld work units is too large", (long long)units);
   // Every job of the launch has the same K-steps (the launches are bucketed by them).
   const int ks = kmax / 32;
   const size_t rec = record_bytes(ks);
+  int64_t pairs = 0;
+  for (auto& j : jobs) pairs += (int64_t)j.bands_n * ((j.rows + ltxw::kPairRows - 1) / ltxw::kPairRows);
+  // The several-LoRA kernel keeps pairs to the end: a mixed DiT block (5
+  // K-steps) measured 251.6-251.9 -> 254.8-255.4 us with single units.
+  if (!multi) split_tail(jobs, pairs, f32out, rec);
+  int64_t units = 0;  // workgroups (unit pairs; single units in a split launch's last job)
+  int64_t main_groups = -1;
+  for (auto& j : jobs) {
+    plan_fused(j);
+    j.unit_begin = units;
+    if (j.single && main_groups < 0) main_groups = units;
+    const int64_t group_rows = j.single ? ltxw::kUnitRows : ltxw::kPairRows;
+    units += (int64_t)j.bands_n * ((j.rows + group_rows - 1) / group_rows);
+  }
+  if (main_groups < 0) main_groups = units;
+  if (units > INT32_MAX) return fail(ctx, LTXW_ERR_INVALID_ARG, "launch of %lld work units is too large", (long long)units);
   const size_t bytes = jobs.size() * rec;
   ltxw::JobTable t{};
   t.n_jobs = (int32_t)jobs.size();
   t.total_units = units;
   t.lds_ld = kmax + 8;
   t.rec_bytes = (int32_t)rec;
+  t.main_groups = (uint32_t)main_groups;
   for (int k = 0; k < ltxw::kInlineBegins; ++k)
     t.begins[k] = (size_t)k < jobs.size() ? (uint32_t)jobs[(size_t)k].unit_begin : UINT32_MAX;
   // The single-LoRA kernel reads a one-job launch's JobDev from its fixed

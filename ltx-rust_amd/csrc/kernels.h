@@ -64,7 +64,7 @@ struct JobDev {
   uint32_t qmask;
   uint32_t cmul;
   float coeff_out;
-  uint32_t pad;
+  uint32_t single;     // 1: one 128-row unit per workgroup (a launch's tail), else a pair
   StepDev step[kMaxSteps];
 };
 
@@ -80,7 +80,7 @@ struct FusedJob {
   uint32_t unit_begin;  // first workgroup of this job in the launch
   uint32_t fmt, scale_mode, qmask, cmul;
   float coeff_out;
-  uint32_t pad;
+  uint32_t single;      // JobDev::single
 };
 static_assert(sizeof(FusedJob) == 64 && sizeof(StepDev) == 32, "record layout");
 
@@ -97,7 +97,8 @@ struct JobTable {
   int32_t lds_ld;        // AT row stride (bf16): 8 + the launch's largest total padded rank
   int64_t total_units;   // workgroups in the launch
   int32_t rec_bytes;     // bytes per job record: sizeof(FusedJob) + K-steps * sizeof(StepDev)
-  int32_t pad[3];
+  uint32_t main_groups;  // workgroups of the pair jobs; the single-unit jobs follow them
+  int32_t pad[2];
   // unit_begin of the inline records (n_jobs <= kInlineBegins; the rest
   // UINT32_MAX), so that a workgroup finds its record with one load.
   uint32_t begins[kInlineBegins];
@@ -193,6 +194,12 @@ hipError_t launch_fused_multi_base16(const JobTable& t, bool f32out, int ks, hip
 // kernel takes kTileRows rows per workgroup.)
 constexpr int kUnitRows = kWavesPerGroup * kStripRows;
 constexpr int kPairRows = 2 * kUnitRows;
+// Fused launches of more than this many workgroups map workgroups to XCDs
+// in contiguous ranges, and end in single-unit workgroups (kTailPairs).
+constexpr uint32_t kRemapMinGrid = 2048;
+// Pair workgroups' worth of rows at a large launch's end that run as single
+// units instead.
+constexpr int64_t kTailPairs = 512;
 
 // Padded K extent of one LoRA in the fused kernel's LDS stage.
 __host__ __device__ inline int pad_rank(int rank) { return (rank + 31) / 32 * 32; }

@@ -383,6 +383,25 @@ __device__ __forceinline__ void pair_units(const PJ& J, uint16_t* AT, uint32_t i
   }
 }
 
+// One unit per workgroup (the single-unit jobs at a large launch's end):
+// the factors-first order of pair_units without the second unit.
+template <bool F32OUT, int KS, int FMT, bool FULL, bool BSW>
+__device__ __forceinline__ void one_unit(const PJ& J, uint16_t* AT, uint32_t i0, uint32_t g0, int tid) {
+  constexpr int LD = 32 * KS + 8;
+  Stage<KS> st;
+  Frag<KS> f;
+  pp_issue_a<KS>(J, i0, tid, st);
+  pp_issue_f<KS, FULL, BSW>(J, i0, g0, tid, f);
+  __builtin_amdgcn_s_setprio(2);
+  pp_issue_w<KS, FULL>(J, i0, g0, tid, f);
+  __builtin_amdgcn_s_setprio(0);
+  pp_stage<KS>(st, AT, LD, tid);
+  __syncthreads();
+  Acc<KS> acc;
+  pp_mfma<KS, BSW>(J, f, AT, LD, tid, acc);
+  pp_epilogue<F32OUT, KS, FULL, FMT, true>(J, f, acc, i0, g0, tid);
+}
+
 // One workgroup per unit pair; the jobs' unit_begin count pairs. BSW: the
 // B-fragment pair swap (launches of kSwapMinGrid workgroups and more);
 // WFIRST: FP8 bytes before factors (launches of at most kWFirstMaxGrid).
@@ -390,10 +409,24 @@ template <bool F32OUT, int KS, bool BSW, bool WFIRST>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS == 1 || (KS == 2 && WFIRST) ? 3 : 2))) void k_fused_pair(JobTable tab) {
   extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
   const int tid = threadIdx.x;
-  const uint32_t pair = xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t pair = xcd_remap(blockIdx.x, gridDim.x, tab.main_groups);
   const PJ J = pj_load<KS>(tab, pair);
   const uint32_t p = pair - J.unit_begin;
   const uint32_t i0 = (p % J.bands_n) * kBandCols;
+  if constexpr (!WFIRST) {
+    if (J.single) {
+      const uint32_t g0 = (p / J.bands_n) * kUnitRows;
+      const bool full1 = g0 + kUnitRows <= J.rows && i0 + kBandCols <= J.cols;
+      if (J.fmt == 0) {
+        if (full1) one_unit<F32OUT, KS, 0, true, BSW>(J, AT, i0, g0, tid);
+        else one_unit<F32OUT, KS, 0, false, BSW>(J, AT, i0, g0, tid);
+      } else {
+        if (full1) one_unit<F32OUT, KS, 1, true, BSW>(J, AT, i0, g0, tid);
+        else one_unit<F32OUT, KS, 1, false, BSW>(J, AT, i0, g0, tid);
+      }
+      return;
+    }
+  }
   const uint32_t gA = (p / J.bands_n) * (2 * kWavesPerGroup * kStripRows);
   const uint32_t gB = gA + kWavesPerGroup * kStripRows;
   const bool hasB = gB < J.rows;

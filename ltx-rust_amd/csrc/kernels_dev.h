@@ -138,8 +138,8 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* G(T* p) {
 // their LoRA B rows in that XCD's L2). A bijection on [0, n). Launches of up
 // to kRemapMinGrid workgroups (a few layers, resident at once or nearly)
 // keep the dispatch order: measured 2-5% faster there (one 4096 x 4096 layer
-// 12.5 -> 11.9 us), while the remap wins from about a DiT block up.
-constexpr uint32_t kRemapMinGrid = 2048;
+// 12.5 -> 11.9 us), while the remap wins from about a DiT block up
+// (kRemapMinGrid, kernels.h).
 // Launches of at least this many workgroups use the B-fragment pair swap
 // (BSW, below): measured 2% faster on two 4096 x 4096 layers (1024
 // workgroups), 1.5-2% on four layers or an FFN matrix (2048), 1-3% per DiT
@@ -151,10 +151,13 @@ constexpr int64_t kSwapMinGrid = 1024;
 // factors: one 4096 x 4096 layer 11.8-12.2 -> 11.7-11.8 us; from four layers
 // up the factors-first order is 1-3% faster.
 constexpr int64_t kWFirstMaxGrid = 512;
-__device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t n) {
-  if (n <= kRemapMinGrid) return bid;
+// `main`: the workgroups of the launch's pair jobs. Workgroups from `main` on
+// (the single-unit jobs at the launch's end) keep their order, so the last
+// workgroups each XCD starts are narrow ones.
+__device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t n, uint32_t main) {
+  if (n <= kRemapMinGrid || bid >= main) return bid;
   constexpr uint32_t kXcd = 8;
-  uint32_t per = n / kXcd, rem = n % kXcd;
+  uint32_t per = main / kXcd, rem = main % kXcd;
   uint32_t x = bid % kXcd, k = bid / kXcd;
   return x < rem ? x * (per + 1) + k : rem * (per + 1) + (x - rem) * per + k;
 }
@@ -276,6 +279,7 @@ struct PJ {
   uint32_t cmul;  // coeff applies (coeff != 1)
   uint32_t unit_begin;
   float tscale;   // the per-tensor scale (scale_mode 1), else 1
+  uint32_t single;  // one unit per workgroup
 };
 
 template <int KS>
@@ -299,6 +303,7 @@ __device__ __forceinline__ PJ pj_load(const JobTable& t, uint32_t wg) {
     p.coeff = __builtin_bit_cast(float, uni(__builtin_bit_cast(uint32_t, J.coeff_out)));
     p.cmul = uni(J.cmul);
     p.unit_begin = uni((uint32_t)J.unit_begin);
+    p.single = 0;  // a split launch has several jobs
   } else {
     CByte* rec = job_record<KS>(t, wg);
     const FusedJob J = kload<FusedJob>(rec);
@@ -317,6 +322,7 @@ __device__ __forceinline__ PJ pj_load(const JobTable& t, uint32_t wg) {
     p.coeff = J.coeff_out;
     p.cmul = J.cmul;
     p.unit_begin = J.unit_begin;
+    p.single = J.single;
   }
   // One uniform load at the start: no per-lane load in the scale branch of
   // the factor issue (a vector load on one path only costs waits on both).

@@ -96,6 +96,7 @@ __device__ __forceinline__ PJM<KS> pjm_load(const JobTable& t, uint32_t wg) {
   m.base.coeff = J.coeff_out;
   m.base.cmul = J.cmul;
   m.base.unit_begin = J.unit_begin;
+  m.base.single = 0;  // no single-unit jobs in several-LoRA launches
   m.pf = 0;
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
@@ -341,7 +342,7 @@ template <bool F32OUT, int KS, int FDT, bool B16, bool BSW, bool WFIRST>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_fused_pair_multi(JobTable tab) {
   extern __shared__ __attribute__((aligned(16))) uint16_t AT[];
   const int tid = threadIdx.x;
-  const uint32_t pair = xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t pair = xcd_remap(blockIdx.x, gridDim.x, tab.main_groups);
   const PJM<KS> M = pjm_load<KS, BSW>(tab, pair);
   const uint32_t p = pair - M.base.unit_begin;
   const uint32_t i0 = (p % M.base.bands_n) * kBandCols;
