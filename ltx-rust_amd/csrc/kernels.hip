@@ -402,7 +402,8 @@ __device__ __forceinline__ void one_unit(const PJ& J, uint16_t* AT, uint32_t i0,
   pp_epilogue<F32OUT, KS, FULL, FMT, true>(J, f, acc, i0, g0, tid);
 }
 
-// One workgroup per unit pair; the jobs' unit_begin count pairs. BSW: the
+// One workgroup per unit pair (per unit in a `single` job); the jobs'
+// unit_begin count workgroups. BSW: the
 // B-fragment pair swap (launches of kSwapMinGrid workgroups and more);
 // WFIRST: FP8 bytes before factors (launches of at most kWFirstMaxGrid).
 template <bool F32OUT, int KS, bool BSW, bool WFIRST>
