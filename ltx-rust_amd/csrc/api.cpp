@@ -387,9 +387,11 @@ int run_fused(ltxw_ctx* ctx, std::vector<ltxw::JobDev>& jobs, bool f32out, bool 
   const size_t rec = record_bytes(ks);
   int64_t pairs = 0;
   for (auto& j : jobs) pairs += (int64_t)j.bands_n * ((j.rows + ltxw::kPairRows - 1) / ltxw::kPairRows);
-  // The several-LoRA kernel keeps pairs to the end: a mixed DiT block (5
-  // K-steps) measured 251.6-251.9 -> 254.8-255.4 us with single units.
-  if (!multi) split_tail(jobs, pairs, f32out, rec);
+  // Several-LoRA launches split up to 2 K-steps (a DiT block with r32 + r32
+  // LoRAs 151.3-153.1 -> 147.0-147.6 us) and keep pairs to the end above: a
+  // mixed DiT block (5 K-steps) measured 251.6-251.9 -> 254.8-255.4 us with
+  // single units.
+  if (!multi || ks <= 2) split_tail(jobs, pairs, f32out, rec);
   int64_t units = 0;  // workgroups (unit pairs; single units in a split launch's last job)
   int64_t main_groups = -1;
   for (auto& j : jobs) {

@@ -195,8 +195,8 @@ hipError_t launch_fused_multi_base16(const JobTable& t, bool f32out, int ks, hip
 constexpr int kUnitRows = kWavesPerGroup * kStripRows;
 constexpr int kPairRows = 2 * kUnitRows;
 // Fused launches of more than this many workgroups map workgroups to XCDs
-// in contiguous ranges; single-LoRA ones also end in single-unit workgroups
-// (kTailPairs).
+// in contiguous ranges; those of at most 2 K-steps, and every single-LoRA
+// one, also end in single-unit workgroups (kTailPairs).
 constexpr uint32_t kRemapMinGrid = 2048;
 // Pair workgroups' worth of rows at a large launch's end that run as single
 // units instead.

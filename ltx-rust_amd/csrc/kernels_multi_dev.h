@@ -96,7 +96,7 @@ __device__ __forceinline__ PJM<KS> pjm_load(const JobTable& t, uint32_t wg) {
   m.base.coeff = J.coeff_out;
   m.base.cmul = J.cmul;
   m.base.unit_begin = J.unit_begin;
-  m.base.single = 0;  // no single-unit jobs in several-LoRA launches
+  m.base.single = J.single;
   m.pf = 0;
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
@@ -335,6 +335,26 @@ __device__ __forceinline__ void pair_units_multi(const PJM<KS>& M, uint16_t* AT,
   }
 }
 
+// One unit per workgroup (the single-unit jobs at a large launch's end), as
+// one_unit (kernels.hip).
+template <bool F32OUT, int KS, int FMT, bool FULL, int FDT, bool BSW>
+__device__ __forceinline__ void one_unit_multi(const PJM<KS>& M, uint16_t* AT, uint32_t i0, uint32_t g0, int tid) {
+  constexpr int LD = 32 * KS + 8;
+  constexpr bool B16 = FMT >= 2;
+  StageM<KS, FDT> st;
+  FragM<KS, FDT, B16> f;
+  pm_issue_a<KS, FDT>(M, i0, tid, st);
+  pm_issue_f<KS, FULL, FDT, B16, BSW>(M, g0, tid, f);
+  __builtin_amdgcn_s_setprio(2);
+  pp_issue_w<KS, FULL>(M.base, i0, g0, tid, f);
+  __builtin_amdgcn_s_setprio(0);
+  pm_stage<KS, FDT>(st, AT, LD, tid);
+  __syncthreads();
+  Acc<KS> acc;
+  pm_mfma<KS, FDT, B16, BSW>(M, f, AT, LD, tid, acc);
+  pp_epilogue<F32OUT, KS, FULL, FMT, true>(M.base, f, acc, i0, g0, tid);
+}
+
 // BSW: the B-fragment pair swap (launches of kSwapMinGrid workgroups and
 // more, 16-bit factors); WFIRST: base bytes before factors (launches of at
 // most kWFirstMaxGrid workgroups, up to 2 K-steps).
@@ -346,12 +366,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   const PJM<KS> M = pjm_load<KS, BSW>(tab, pair);
   const uint32_t p = pair - M.base.unit_begin;
   const uint32_t i0 = (p % M.base.bands_n) * kBandCols;
+  // Base formats (ltxw_format): e4m3fn / e5m2, or with B16 bf16 / f16.
+  constexpr int F0 = B16 ? 2 : 0, F1 = B16 ? 3 : 1;
+  if constexpr (!WFIRST && KS <= 2) {
+    if (M.base.single) {
+      const uint32_t g0 = (p / M.base.bands_n) * kUnitRows;
+      const bool full1 = g0 + kUnitRows <= M.base.rows && i0 + kBandCols <= M.base.cols;
+      if (M.base.fmt == (uint32_t)F0) {
+        if (full1) one_unit_multi<F32OUT, KS, F0, true, FDT, BSW>(M, AT, i0, g0, tid);
+        else one_unit_multi<F32OUT, KS, F0, false, FDT, BSW>(M, AT, i0, g0, tid);
+      } else {
+        if (full1) one_unit_multi<F32OUT, KS, F1, true, FDT, BSW>(M, AT, i0, g0, tid);
+        else one_unit_multi<F32OUT, KS, F1, false, FDT, BSW>(M, AT, i0, g0, tid);
+      }
+      return;
+    }
+  }
   const uint32_t gA = (p / M.base.bands_n) * (2 * kWavesPerGroup * kStripRows);
   const uint32_t gB = gA + kWavesPerGroup * kStripRows;
   const bool hasB = gB < M.base.rows;
   const bool full = gB + kWavesPerGroup * kStripRows <= M.base.rows && i0 + kBandCols <= M.base.cols;
-  // Base formats (ltxw_format): e4m3fn / e5m2, or with B16 bf16 / f16.
-  constexpr int F0 = B16 ? 2 : 0, F1 = B16 ? 3 : 1;
   if (M.base.fmt == (uint32_t)F0) {
     if (full) pair_units_multi<F32OUT, KS, F0, true, FDT, BSW, WFIRST>(M, AT, i0, gA, gB, hasB, tid);
     else pair_units_multi<F32OUT, KS, F0, false, FDT, BSW, WFIRST>(M, AT, i0, gA, gB, hasB, tid);
